@@ -1,0 +1,88 @@
+"""torch.library custom ops: drop-in for src_ii/attention_srcii.py of sqcu/futudiffu.
+
+Registers the same op names and schemas the reference registers
+(src_ii/attention_srcii.py:54-64 and :109-119):
+
+    futudiffu_ii::sage_attn_masked(q, k, v, block_mask, sm_scale) -> (out, lse)
+    futudiffu_ii::sage_attn(q, k, v, sm_scale)                    -> (out, lse)
+
+with identical fake (meta) implementations: contiguous ``[B, H, N, D]`` output
+and ``[B*H, N]`` fp32 LSE.  The masked op is int8-QK / bf16-PV like the
+production kernel it replaces (sage_attention.py:521-529); the unmasked op uses
+the ``configure_sage`` selection (sage_attention.py:271-341).
+
+``futudiffu_ii::sage_attn_ext`` exposes every variant as op arguments
+(qk, pv, granularity, smoothing, optional tile mask, optional exact doc ids).
+
+Backward is not part of this forward-only build: the ops register an autograd
+formula that raises, so a training graph fails loudly instead of silently
+dropping gradients (the reference wires Triton backward kernels here,
+attention_srcii.py:36-84).
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from .sage_attention import sage_attn_forward_masked_with_lse, sage_attn_forward_with_lse, sage_forward
+
+
+def _fake_out(q: Tensor) -> tuple[Tensor, Tensor]:
+    B, H, N, D = q.shape
+    return q.new_empty(B, H, N, D), q.new_empty(B * H, N, dtype=torch.float32)
+
+
+def _no_backward(ctx, grad_out, grad_lse):
+    raise NotImplementedError("Sage attention backward is not implemented in the MI355X build "
+                              "(forward-only); run training with the reference backward kernels")
+
+
+def _setup_context(ctx, inputs, output):
+    pass
+
+
+@torch.library.custom_op("futudiffu_ii::sage_attn_masked", mutates_args=())
+def sage_attn_masked_op(q: Tensor, k: Tensor, v: Tensor, block_mask: Tensor,
+                        sm_scale: float) -> tuple[Tensor, Tensor]:
+    out, lse = sage_attn_forward_masked_with_lse(q, k, v, block_mask, sm_scale)
+    return out, lse
+
+
+@sage_attn_masked_op.register_fake
+def _fake_fwd_masked(q, k, v, block_mask, sm_scale):
+    return _fake_out(q)
+
+
+sage_attn_masked_op.register_autograd(_no_backward, setup_context=_setup_context)
+
+
+@torch.library.custom_op("futudiffu_ii::sage_attn", mutates_args=())
+def sage_attn_op(q: Tensor, k: Tensor, v: Tensor, sm_scale: float) -> tuple[Tensor, Tensor]:
+    out, lse = sage_attn_forward_with_lse(q, k, v, sm_scale)
+    return out, lse
+
+
+@sage_attn_op.register_fake
+def _fake_fwd(q, k, v, sm_scale):
+    return _fake_out(q)
+
+
+sage_attn_op.register_autograd(_no_backward, setup_context=_setup_context)
+
+
+@torch.library.custom_op("futudiffu_ii::sage_attn_ext", mutates_args=())
+def sage_attn_ext_op(q: Tensor, k: Tensor, v: Tensor, block_mask: Tensor | None, doc_ids: Tensor | None,
+                     sm_scale: float, qk: str, pv: str, granularity: str,
+                     smooth_k: bool) -> tuple[Tensor, Tensor]:
+    out, lse = sage_forward(q, k, v, sm_scale, block_mask=block_mask, doc_ids=doc_ids, qk=qk, pv=pv,
+                            granularity=granularity, smooth_k=smooth_k)
+    return out, lse
+
+
+@sage_attn_ext_op.register_fake
+def _fake_ext(q, k, v, block_mask, doc_ids, sm_scale, qk, pv, granularity, smooth_k):
+    return _fake_out(q)
+
+
+sage_attn_ext_op.register_autograd(_no_backward, setup_context=_setup_context)

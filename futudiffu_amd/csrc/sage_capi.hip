@@ -1,0 +1,152 @@
+// extern "C" boundary of libsage_mi355x.so: argument validation, error
+// reporting and dispatch to the gfx950 kernels.  See include/sage_mi355x.h.
+#include <stdio.h>
+#include <stdarg.h>
+#include <string.h>
+
+#include "../../include/sage_mi355x.h"
+#include "sage_common.h"
+
+#include "sage_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(int64_t bh, int64_t n, int64_t d, int qk, int pv, int gran) {
+  if (bh <= 0 || n <= 0) return fail(SAGE_ERR_ARG, "bh=%lld and n=%lld must be positive", (long long)bh, (long long)n);
+  if (d != 64 && d != 128) return fail(SAGE_ERR_ARG, "head_dim must be 64 or 128, got %lld", (long long)d);
+  if (qk != SAGE_QK_INT8 && qk != SAGE_QK_FP8) return fail(SAGE_ERR_ARG, "unknown qk_kind %d", qk);
+  if (pv != SAGE_PV_BF16 && pv != SAGE_PV_FP8) return fail(SAGE_ERR_ARG, "unknown pv_kind %d", pv);
+  if (gran != SAGE_GRAN_TOKEN && gran != SAGE_GRAN_BLOCK64) return fail(SAGE_ERR_ARG, "unknown granularity %d", gran);
+  if (bh > 65535) return fail(SAGE_ERR_ARG, "bh=%lld exceeds the grid limit 65535", (long long)bh);
+  if (n > (int64_t)1 << 24) return fail(SAGE_ERR_ARG, "n=%lld exceeds 2^24", (long long)n);
+  return SAGE_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(SAGE_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  g_err[0] = '\0';
+  return SAGE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sage_abi_version(void) { return SAGE_ABI_VERSION; }
+
+const char* sage_last_error(void) { return g_err; }
+
+int64_t sage_padded_len(int64_t n) { return sage::padded_len(n); }
+
+size_t sage_quant_workspace_bytes(int64_t bh, int64_t n, int64_t d) { return sage::quant_workspace_bytes(bh, n, d); }
+
+size_t sage_attn_workspace_bytes(int64_t b, int64_t n) { return sage::attn_workspace_bytes(b, n); }
+
+int sage_quantize_qkv(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t d, int qk_kind,
+                      int pv_kind, int granularity, int smooth_k, float sm_scale_log2e, void* q_codes,
+                      float* q_scale, void* k_codes, float* k_scale, void* v_out, float* v_scale, void* k_mean,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = check_common(bh, n, d, qk_kind, pv_kind, granularity);
+  if (st) return st;
+  if (!q || !k || !v || !q_codes || !q_scale || !k_codes || !k_scale || !v_out)
+    return fail(SAGE_ERR_ARG, "null tensor pointer");
+  if (pv_kind == SAGE_PV_FP8 && !v_scale) return fail(SAGE_ERR_ARG, "fp8 PV needs v_scale");
+  const void* ptrs[] = {q, k, v, q_codes, q_scale, k_codes, k_scale, v_out};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
+  if (v_scale && !aligned16(v_scale)) return fail(SAGE_ERR_ALIGN, "v_scale must be 16-byte aligned");
+  if (smooth_k) {
+    if (!k_mean) return fail(SAGE_ERR_ARG, "smooth_k needs k_mean");
+    const size_t need = sage::quant_workspace_bytes(bh, n, d);
+    if (!workspace || workspace_bytes < need)
+      return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+  }
+  hipError_t e = sage::launch_quantize(
+      qk_kind, pv_kind, granularity, smooth_k != 0, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+      static_cast<const uint16_t*>(v), bh, n, d, sm_scale_log2e, static_cast<double*>(workspace),
+      static_cast<uint8_t*>(q_codes), q_scale, static_cast<uint8_t*>(k_codes), k_scale, static_cast<uint8_t*>(v_out),
+      v_scale, static_cast<uint16_t*>(k_mean), stream);
+  return launch_status(e, "sage_quantize_qkv");
+}
+
+int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,
+                  const void* v_in, const float* v_scale, int64_t b, int64_t h, int64_t n, int64_t d, int qk_kind,
+                  int pv_kind, int granularity, const uint8_t* tile_mask, int64_t mask_stride_z, int64_t mask_nq,
+                  int64_t mask_nkv, const int32_t* doc_ids, void* workspace, size_t workspace_bytes, void* out,
+                  float* lse, hipStream_t stream) {
+  if (b <= 0 || h <= 0) return fail(SAGE_ERR_ARG, "b=%lld and h=%lld must be positive", (long long)b, (long long)h);
+  int st = check_common(b * h, n, d, qk_kind, pv_kind, granularity);
+  if (st) return st;
+  if (!q_codes || !q_scale || !k_codes || !k_scale || !v_in || !out || !lse)
+    return fail(SAGE_ERR_ARG, "null tensor pointer");
+  if (pv_kind == SAGE_PV_FP8 && !v_scale) return fail(SAGE_ERR_ARG, "fp8 PV needs v_scale");
+  const void* ptrs[] = {q_codes, q_scale, k_codes, k_scale, v_in, out};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
+  if (v_scale && !aligned16(v_scale)) return fail(SAGE_ERR_ALIGN, "v_scale must be 16-byte aligned");
+  const int64_t nq = (n + 127) / 128, nkv = (n + 63) / 64;
+  int mask = 0;
+  if (tile_mask) {
+    if (mask_nq != nq || mask_nkv != nkv)
+      return fail(SAGE_ERR_ARG, "block_mask must be %lld x %lld tiles, got %lld x %lld", (long long)nq,
+                  (long long)nkv, (long long)mask_nq, (long long)mask_nkv);
+    if (mask_stride_z != 0 && mask_stride_z != nq * nkv)
+      return fail(SAGE_ERR_ARG, "mask_stride_z must be 0 (2D mask) or %lld (3D mask)", (long long)(nq * nkv));
+    mask |= 1;
+  }
+  sage::AttnParams p;
+  memset(&p, 0, sizeof(p));
+  if (doc_ids) {
+    const size_t need = sage::attn_workspace_bytes(b, n);
+    if (!workspace || workspace_bytes < need)
+      return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+    if (!aligned16(workspace)) return fail(SAGE_ERR_ALIGN, "workspace must be 16-byte aligned");
+    mask |= 2;
+    const int64_t nt = nkv;
+    p.kv_sum = static_cast<const int4*>(workspace);
+    p.q_sum = static_cast<const int4*>(workspace) + b * nt;
+  }
+  p.qc = static_cast<const uint8_t*>(q_codes);
+  p.qs = q_scale;
+  p.kc = static_cast<const uint8_t*>(k_codes);
+  p.ks = k_scale;
+  p.vin = static_cast<const uint8_t*>(v_in);
+  p.vs = v_scale;
+  p.tile_mask = tile_mask;
+  p.mask_stride_z = mask_stride_z;
+  p.mask_nkv = mask_nkv;
+  p.doc = doc_ids;
+  p.out = static_cast<uint16_t*>(out);
+  p.lse = lse;
+  p.n = n;
+  p.np = sage::padded_len(n);
+  p.h = (int)h;
+  p.nt = (int)nkv;
+  hipError_t e = sage::launch_attn(qk_kind, pv_kind, granularity, mask, p, b * h, d, (int)b, stream);
+  return launch_status(e, "sage_attn_fwd");
+}
+
+int sage_qk_int32(const void* q_codes, const void* k_codes, int64_t bh, int64_t n, int64_t d, int32_t* s_out,
+                  hipStream_t stream) {
+  int st = check_common(bh, n, d, SAGE_QK_INT8, SAGE_PV_BF16, SAGE_GRAN_TOKEN);
+  if (st) return st;
+  if (!q_codes || !k_codes || !s_out) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  if (!aligned16(q_codes) || !aligned16(k_codes)) return fail(SAGE_ERR_ALIGN, "codes must be 16-byte aligned");
+  hipError_t e = sage::launch_qk_int32(static_cast<const uint8_t*>(q_codes), static_cast<const uint8_t*>(k_codes),
+                                       bh, n, d, s_out, stream);
+  return launch_status(e, "sage_qk_int32");
+}
+
+}  // extern "C"

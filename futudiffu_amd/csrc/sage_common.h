@@ -1,0 +1,66 @@
+// Shared device helpers for the gfx950 Sage attention kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sage {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kQK_INT8 = 0, kQK_FP8 = 1;
+constexpr int kPV_BF16 = 0, kPV_FP8 = 1;
+constexpr int kGRAN_TOKEN = 0, kGRAN_BLOCK64 = 1;
+
+constexpr int kRowsPerWG = 128;  // query rows per workgroup = reference Q tile (block_mask.py:27)
+constexpr int kKVTile = 64;      // keys per tile = reference KV tile (block_mask.py:28)
+constexpr float kEps = 1e-12f;   // tl.maximum(amax, 1e-12) (sage_kernels.py:1421)
+constexpr float kFp8Max = 448.0f;
+constexpr float kInt8Max = 127.0f;
+
+__host__ __device__ inline int64_t padded_len(int64_t n) { return (n + 127) / 128 * 128; }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (the rounding torch uses for bf16 results).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Two fp32 -> two OCP e4m3fn codes (RNE, saturating) packed into 16 bits.
+__device__ __forceinline__ uint32_t pack_fp8x2(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+
+__device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+// Truncating fp32 -> int8 (Triton .to(tl.int8) lowers to fptosi), packed.
+__device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d) {
+  uint32_t x0 = (uint32_t)((int)a) & 0xffu;
+  uint32_t x1 = (uint32_t)((int)b) & 0xffu;
+  uint32_t x2 = (uint32_t)((int)c) & 0xffu;
+  uint32_t x3 = (uint32_t)((int)d) & 0xffu;
+  return x0 | (x1 << 8) | (x2 << 16) | (x3 << 24);
+}
+
+// Byte offset of the 16-byte piece of row-fragment code storage that holds
+// token `tok`, channels [32*c + 16*h, +16).  See include/sage_mi355x.h.
+__host__ __device__ __forceinline__ int64_t row_frag_offset(int64_t tok, int c, int h, int d) {
+  const int64_t rb = tok >> 5;
+  const int r = (int)(tok & 31);
+  return ((rb * (d / 32) + c) * 64 + (h * 32 + r)) * 16;
+}
+
+}  // namespace sage

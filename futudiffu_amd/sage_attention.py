@@ -1,0 +1,247 @@
+"""SageAttention forward on MI355X: host-side mirror of the reference API.
+
+Mirrors ``src/futudiffu/sage_attention.py`` of sqcu/futudiffu (function names,
+argument meaning and error behaviour) on top of the gfx950 HIP library
+``libsage_mi355x.so``:
+
+* ``configure_sage`` / module defaults     -> sage_attention.py:32-60
+* ``sage_attn_forward``                    -> :121-180
+* ``sage_attn_forward_masked``             -> :183-268
+* ``sage_attn_forward_with_lse``           -> :271-341
+* ``sage_attn_forward_masked_with_lse``    -> :461-531
+
+Each call runs two kernels on the current stream: ``sage_quantize_qkv``
+(K smoothing + Q/K/V quantization) and ``sage_attn_fwd``.  All outputs and
+temporaries are allocated through the PyTorch caching allocator; nothing
+synchronizes the host.  Variant choice (qk int8/fp8, pv bf16/fp8, scale
+granularity, smoothing, exact doc-id masking) is also available as explicit
+keyword arguments of :func:`sage_forward`, which the module-level
+configuration only supplies defaults for.
+
+Differences from the reference, all deliberate:
+* head_dim 64 is accepted as well as 128 (reference asserts 128,
+  sage_attention.py:487);
+* ``pv="fp8"`` honours ``qk`` (the reference's unmasked LSE path always uses
+  fp8 QK with fp8 PV, sage_attention.py:316-323), so int8-QK/fp8-PV exists;
+* rows that see no key return 0 and LSE = -inf instead of NaN.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_LOG2E = math.log2(math.e)
+
+_SAGE_SMOOTH_K = True
+_SAGE_QK_QUANT = "fp8"
+_SAGE_PV_QUANT = "bf16"
+
+_QK = {"int8": 0, "fp8": 1}
+_PV = {"bf16": 0, "fp8": 1}
+_GRAN = {"token": 0, "block64": 1}
+
+
+def configure_sage(*, smooth_k: bool = True, qk_quant: str = "fp8", pv_quant: str = "bf16") -> None:
+    """Select the defaults used by the no-keyword entry points (sage_attention.py:37-60)."""
+    global _SAGE_SMOOTH_K, _SAGE_QK_QUANT, _SAGE_PV_QUANT
+    if qk_quant not in ("fp8", "int8"):
+        raise ValueError(f"Unknown qk_quant: {qk_quant!r}")
+    if pv_quant not in ("bf16", "fp8"):
+        raise ValueError(f"Unknown pv_quant: {pv_quant!r}")
+    _SAGE_SMOOTH_K = smooth_k
+    _SAGE_QK_QUANT = qk_quant
+    _SAGE_PV_QUANT = pv_quant
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check_inputs(q: Tensor, k: Tensor, v: Tensor) -> tuple[int, int, int, int]:
+    if q.ndim != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must share one [B, H, N, D] shape, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    B, H, N, D = q.shape
+    assert D in (64, 128), f"SageAttention on MI355X requires head_dim 64 or 128, got {D}"
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        assert t.dtype == torch.bfloat16, f"Expected BF16 input, got {t.dtype} for {name}"
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a GPU tensor (device {t.device})")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q, k, v must be on one device")
+    return B, H, N, D
+
+
+@dataclass
+class SageQuantized:
+    """Device tensors produced by ``sage_quantize_qkv`` (fragment storage order)."""
+    q_codes: Tensor       # uint8 [BH, Np*D]
+    q_scale: Tensor       # fp32 [BH, Np] or [BH, Np/64]
+    k_codes: Tensor
+    k_scale: Tensor
+    v_op: Tensor          # fp8 codes (uint8 [BH, Np*D]) or bf16 fragments ([BH, Np*D])
+    v_scale: Tensor | None
+    k_mean: Tensor | None  # bf16 [BH, D]
+    qk: str
+    pv: str
+    granularity: str
+    n: int
+    np_: int
+    d: int
+
+
+def quantize_qkv(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None, *,
+                 qk: str = "int8", pv: str = "bf16", granularity: str = "token",
+                 smooth_k: bool = True) -> SageQuantized:
+    """Smoothing + quantization of q, k, v (``[B, H, N, D]`` bf16) on the GPU."""
+    B, H, N, D = _check_inputs(q, k, v)
+    if qk not in _QK or pv not in _PV or granularity not in _GRAN:
+        raise ValueError(f"bad variant qk={qk!r} pv={pv!r} granularity={granularity!r}")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    lib = _lib.load()
+    BH = B * H
+    Np = int(lib.sage_padded_len(N))
+    dev = q.device
+    q3, k3, v3 = (t.reshape(BH, N, D).contiguous() for t in (q, k, v))
+    ns = Np if granularity == "token" else Np // 64
+    qc = torch.empty(BH, Np * D, dtype=torch.uint8, device=dev)
+    kc = torch.empty_like(qc)
+    qs = torch.empty(BH, ns, dtype=torch.float32, device=dev)
+    ks = torch.empty_like(qs)
+    if pv == "fp8":
+        vop = torch.empty(BH, Np * D, dtype=torch.uint8, device=dev)
+        vs = torch.empty(BH, Np // 64, D, dtype=torch.float32, device=dev)
+    else:
+        vop = torch.empty(BH, Np * D, dtype=torch.bfloat16, device=dev)
+        vs = None
+    km = torch.empty(BH, D, dtype=torch.bfloat16, device=dev) if smooth_k else None
+    wsb = int(lib.sage_quant_workspace_bytes(BH, N, D)) if smooth_k else 0
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev) if smooth_k else None
+    fold = float(torch.tensor(sm_scale * _LOG2E, dtype=torch.float32))
+    _lib.check(lib.sage_quantize_qkv(
+        q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), BH, N, D,
+        _QK[qk], _PV[pv], _GRAN[granularity], int(smooth_k), fold,
+        qc.data_ptr(), qs.data_ptr(), kc.data_ptr(), ks.data_ptr(),
+        vop.data_ptr(), _ptr(vs), _ptr(km), _ptr(ws), wsb, _stream_handle(dev)))
+    return SageQuantized(qc, qs, kc, ks, vop, vs, km, qk, pv, granularity, N, Np, D)
+
+
+def _norm_mask(block_mask: Tensor | None, BH: int, N: int, device) -> tuple[Tensor | None, int, int, int]:
+    if block_mask is None:
+        return None, 0, 0, 0
+    bm = block_mask
+    if bm.dtype != torch.uint8:
+        bm = bm.to(torch.uint8)
+    bm = bm.to(device).contiguous()
+    if bm.ndim == 2:
+        stride_z = 0
+        nq, nkv = bm.shape
+    elif bm.ndim == 3:
+        if bm.shape[0] != BH:
+            raise ValueError(f"3D block_mask must have B*H={BH} rows, got {bm.shape[0]}")
+        nq, nkv = bm.shape[1], bm.shape[2]
+        stride_z = nq * nkv
+    else:
+        raise ValueError(f"block_mask must be 2D or 3D, got {bm.ndim}D")
+    return bm, stride_z, nq, nkv
+
+
+def attn_from_quantized(qz: SageQuantized, B: int, H: int, *, block_mask: Tensor | None = None,
+                        doc_ids: Tensor | None = None, out: Tensor | None = None,
+                        lse: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """Run the fused attention kernel on quantized operands; returns (out, lse)."""
+    lib = _lib.load()
+    BH, N, D = B * H, qz.n, qz.d
+    dev = qz.q_codes.device
+    bm, stride_z, nq, nkv = _norm_mask(block_mask, BH, N, dev)
+    ws = None
+    wsb = 0
+    if doc_ids is not None:
+        if doc_ids.shape != (B, N):
+            raise ValueError(f"doc_ids must be [B, N] = [{B}, {N}], got {tuple(doc_ids.shape)}")
+        doc_ids = doc_ids.to(device=dev, dtype=torch.int32).contiguous()
+        wsb = int(lib.sage_attn_workspace_bytes(B, N))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    if out is None:
+        out = torch.empty(B, H, N, D, dtype=torch.bfloat16, device=dev)
+    if lse is None:
+        lse = torch.empty(BH, N, dtype=torch.float32, device=dev)
+    _lib.check(lib.sage_attn_fwd(
+        qz.q_codes.data_ptr(), qz.q_scale.data_ptr(), qz.k_codes.data_ptr(), qz.k_scale.data_ptr(),
+        qz.v_op.data_ptr(), _ptr(qz.v_scale), B, H, N, D, _QK[qz.qk], _PV[qz.pv], _GRAN[qz.granularity],
+        _ptr(bm), stride_z, nq, nkv, _ptr(doc_ids), _ptr(ws), wsb, out.data_ptr(), lse.data_ptr(),
+        _stream_handle(dev)))
+    return out, lse
+
+
+def sage_forward(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None, *,
+                 block_mask: Tensor | None = None, doc_ids: Tensor | None = None,
+                 qk: str | None = None, pv: str | None = None, granularity: str = "token",
+                 smooth_k: bool | None = None) -> tuple[Tensor, Tensor]:
+    """Sage forward with explicit variant selection; returns ``(out [B,H,N,D], lse [B*H,N])``."""
+    B, H, N, D = _check_inputs(q, k, v)
+    qk = _SAGE_QK_QUANT if qk is None else qk
+    pv = _SAGE_PV_QUANT if pv is None else pv
+    smooth_k = _SAGE_SMOOTH_K if smooth_k is None else smooth_k
+    if qk not in _QK:
+        raise ValueError(f"Unknown qk_quant: {qk!r}")
+    if pv not in _PV:
+        raise ValueError(f"Unknown pv_quant: {pv!r}")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    qz = quantize_qkv(q, k, v, sm_scale, qk=qk, pv=pv, granularity=granularity, smooth_k=smooth_k)
+    return attn_from_quantized(qz, B, H, block_mask=block_mask, doc_ids=doc_ids)
+
+
+def sage_attn_forward(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None) -> Tensor:
+    """Forward without LSE using the configured QK quantization (sage_attention.py:121-180).
+
+    Like the reference, this legacy entry point always uses bf16 PV.
+    """
+    return sage_forward(q, k, v, sm_scale, pv="bf16")[0]
+
+
+def sage_attn_forward_masked(q: Tensor, k: Tensor, v: Tensor, block_mask: Tensor,
+                             sm_scale: float | None = None) -> Tensor:
+    """Block-masked forward without LSE, bf16 PV (sage_attention.py:183-268)."""
+    return sage_forward(q, k, v, sm_scale, block_mask=block_mask, pv="bf16")[0]
+
+
+def sage_attn_forward_with_lse(q: Tensor, k: Tensor, v: Tensor,
+                               sm_scale: float | None = None) -> tuple[Tensor, Tensor]:
+    """Forward returning (out, lse) with the configured QK and PV (sage_attention.py:271-341)."""
+    return sage_forward(q, k, v, sm_scale)
+
+
+def sage_attn_forward_masked_with_lse(q: Tensor, k: Tensor, v: Tensor, block_mask: Tensor,
+                                      sm_scale: float | None = None, *, qk: str = "int8",
+                                      pv: str = "bf16", granularity: str = "token",
+                                      doc_ids: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """Masked forward with LSE; int8 QK / bf16 PV by default like the production kernel
+    (sage_attention.py:461-531, hard-wired at :521-529)."""
+    return sage_forward(q, k, v, sm_scale, block_mask=block_mask, doc_ids=doc_ids, qk=qk, pv=pv,
+                        granularity=granularity)
+
+
+def qk_int32(q_codes: Tensor, k_codes: Tensor, bh: int, n: int, d: int) -> Tensor:
+    """int32 QK^T of int8 fragment codes through the attention kernel's MFMA path.
+
+    Returns ``[bh, Np, Np]`` int32 (row = query, column = key).
+    """
+    lib = _lib.load()
+    np_ = int(lib.sage_padded_len(n))
+    s = torch.empty(bh, np_, np_, dtype=torch.int32, device=q_codes.device)
+    _lib.check(lib.sage_qk_int32(q_codes.data_ptr(), k_codes.data_ptr(), bh, n, d, s.data_ptr(),
+                                 _stream_handle(q_codes.device)))
+    return s

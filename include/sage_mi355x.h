@@ -1,0 +1,148 @@
+/*
+ * sage_mi355x.h -- C ABI of the MI355X (gfx950) SageAttention forward.
+ *
+ * Drop-in boundary for the attention op that sqcu/futudiffu registers as
+ *   futudiffu_ii::sage_attn_masked(q, k, v, block_mask, sm_scale) -> (out, lse)
+ *   futudiffu_ii::sage_attn(q, k, v, sm_scale)                   -> (out, lse)
+ * (src_ii/attention_srcii.py:54-64 and :109-119).  Those ops call
+ * sage_attn_forward_masked_with_lse / sage_attn_forward_with_lse
+ * (src/futudiffu/sage_attention.py:461-531, :271-341), which smooth K, then
+ * launch one Triton kernel that quantizes Q and K inside the attention loop.
+ * Here the same work is split in two entry points with plain pointers:
+ * sage_quantize_qkv (smoothing + all quantization, memory-bound) and
+ * sage_attn_fwd (8-bit MFMA QK^T, fp32 online softmax, fp8/bf16 PV).
+ *
+ * Every pointer is device memory owned by the caller; the library never
+ * allocates or frees.  Every entry point is stateless, takes the HIP stream to
+ * launch on, never synchronizes, and returns 0 on success or a SAGE_ERR_*
+ * code, with a message available from sage_last_error() (thread-local).
+ *
+ * Tensor layouts (BH = B*H, Np = N rounded up to a multiple of 128):
+ *   q, k, v      bf16 [BH, N, D] contiguous, D in {64, 128}.
+ *   q_codes,
+ *   k_codes      int8 or fp8-e4m3fn codes, BH*Np*D bytes, "row fragment"
+ *                order: for each 32-token block rb, each 32-channel chunk c,
+ *                each lane L = 32*h + r (h in {0,1}, r in [0,32)):
+ *                16 bytes = X[32*rb + r][32*c + 16*h + 0..15].
+ *                Byte offset = ((rb*(D/32) + c)*64 + L)*16.
+ *   q_scale,
+ *   k_scale      fp32; per token [BH, Np] (granularity 0) or per 64-token
+ *                block [BH, Np/64] (granularity 1).  q_scale includes
+ *                sm_scale*log2(e) (sage_kernels.py:1422).
+ *   v_codes      pv_kind 1 (fp8): BH*Np*D bytes; for each 64-token tile t,
+ *                32-channel block j, key half b in {0,1}, lane L = 32*h + r:
+ *                16 bytes, byte 4*jj + i = Vc[64t + 32b + 8jj + 4h + i][32j + r].
+ *                Byte offset = (((t*(D/32) + j)*2 + b)*64 + L)*16.
+ *                pv_kind 0 (bf16): BH*Np*D*2 bytes; for each t, j, b, and
+ *                half tt in {0,1}, lane L: 8 bf16, element 4*jj + i =
+ *                V[64t + 32b + 16tt + 8jj + 4h + i][32j + r].
+ *                Byte offset = ((((t*(D/32) + j)*2 + b)*2 + tt)*64 + L)*16.
+ *   v_scale      fp8 PV only: fp32 [BH, Np/64, D], one scale per (64-token
+ *                block, channel) (sage_kernels.py:1143-1148).
+ *   k_mean       bf16 [BH, D] smoothing mean (written when smooth_k != 0).
+ *   out          bf16 [BH, N, D] contiguous.
+ *   lse          fp32 [BH, N], log2 domain: m + log2(l) in sm_scale*log2(e)
+ *                units (sage_kernels.py:1468-1471).  Rows that see no key
+ *                get out = 0 and lse = -inf.
+ */
+#ifndef SAGE_MI355X_H
+#define SAGE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAGE_ABI_VERSION 1
+
+enum sage_status {
+  SAGE_OK = 0,
+  SAGE_ERR_ARG = 1,         /* bad shape, kind or null pointer            */
+  SAGE_ERR_ALIGN = 2,       /* pointer not 16-byte aligned                 */
+  SAGE_ERR_WORKSPACE = 3,   /* workspace missing or too small              */
+  SAGE_ERR_LAUNCH = 4       /* hipLaunchKernel / hipGetLastError failed    */
+};
+
+enum sage_qk_kind { SAGE_QK_INT8 = 0, SAGE_QK_FP8 = 1 };
+enum sage_pv_kind { SAGE_PV_BF16 = 0, SAGE_PV_FP8 = 1 };
+enum sage_granularity { SAGE_GRAN_TOKEN = 0, SAGE_GRAN_BLOCK64 = 1 };
+
+/* Version of this ABI (SAGE_ABI_VERSION).  No reference counterpart. */
+int sage_abi_version(void);
+
+/* Message for the last non-zero status returned on this thread.
+ * Replaces the reference's Python AssertionError/ValueError text
+ * (sage_attention.py:487-488, :518-519). */
+const char* sage_last_error(void);
+
+/* Np for a sequence length: N rounded up to a multiple of 128. */
+int64_t sage_padded_len(int64_t n);
+
+/* Bytes of device workspace sage_quantize_qkv needs (fp64 partial K sums). */
+size_t sage_quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
+
+/* K smoothing + Q/K (and, for fp8 PV, V) quantization.
+ * Replaces _smooth_k (sage_attention.py:63-71, applied at :490-491) and the
+ * in-kernel Q/K quantization of _sage_attn_fwd_int8qk_bf16pv_masked_lse
+ * (sage_kernels.py:1415-1422, :1443-1449), its fp8 counterparts (:250-258,
+ * :272-280) and the V quantization of _sage_attn_fwd_fp8qk_fp8pv_lse
+ * (:1143-1148).  Codes are bit-exact with those formulas given k_mean.
+ * For pv_kind 0, v_out receives V (bf16, unmodified values) in the bf16
+ * fragment order above and v_scale may be NULL.  sm_scale_log2e is folded
+ * into q_scale (sage_attention.py:493-495).  smooth_k = 0 skips smoothing
+ * (configure_sage(smooth_k=False), sage_attention.py:37-60). */
+int sage_quantize_qkv(const void* q, const void* k, const void* v,
+                      int64_t bh, int64_t n, int64_t d,
+                      int qk_kind, int pv_kind, int granularity, int smooth_k,
+                      float sm_scale_log2e,
+                      void* q_codes, float* q_scale,
+                      void* k_codes, float* k_scale,
+                      void* v_out, float* v_scale,
+                      void* k_mean,
+                      void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+/* Bytes of device workspace sage_attn_fwd needs when doc_ids is given. */
+size_t sage_attn_workspace_bytes(int64_t b, int64_t n);
+
+/* Fused attention forward over pre-quantized operands.
+ * Replaces the launch of _sage_attn_fwd_int8qk_bf16pv_masked_lse
+ * (sage_kernels.py:1378-1477, launched at sage_attention.py:521-529) and the
+ * unmasked dispatch of sage_attn_forward_with_lse (sage_attention.py:316-339).
+ *   tile_mask     optional uint8 reference block mask, entries [z][i][j] for
+ *                 query tile i (128 rows) x key tile j (64 keys); z stride
+ *                 mask_stride_z (0 broadcasts a 2D mask, sage_attention.py:512-519);
+ *                 mask_nq x mask_nkv must equal ceil(N/128) x ceil(N/64).
+ *                 0 skips the tile pair (sage_kernels.py:1428-1436).
+ *   doc_ids       optional int32 [B, N] per-token document ids for exact
+ *                 masking: key n is visible to query m iff doc[n] >= 0 and
+ *                 (doc[m] == doc[n] or doc[m] < 0).  Fully masked tiles issue
+ *                 no MFMA.  Needs workspace of sage_attn_workspace_bytes.
+ *   h             heads per batch (row z of q belongs to batch z / h). */
+int sage_attn_fwd(const void* q_codes, const float* q_scale,
+                  const void* k_codes, const float* k_scale,
+                  const void* v_in, const float* v_scale,
+                  int64_t b, int64_t h, int64_t n, int64_t d,
+                  int qk_kind, int pv_kind, int granularity,
+                  const uint8_t* tile_mask, int64_t mask_stride_z,
+                  int64_t mask_nq, int64_t mask_nkv,
+                  const int32_t* doc_ids,
+                  void* workspace, size_t workspace_bytes,
+                  void* out, float* lse,
+                  hipStream_t stream);
+
+/* Debug/parity: int32 QK^T accumulators of int8 codes through the same MFMA
+ * fragments as sage_attn_fwd, s_out int32 [BH, Np, Np] (row = query).
+ * Replaces the int32 result of tl.dot(q_int8, k_int8) (sage_kernels.py:1451). */
+int sage_qk_int32(const void* q_codes, const void* k_codes,
+                  int64_t bh, int64_t n, int64_t d,
+                  int32_t* s_out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAGE_MI355X_H */

@@ -1,0 +1,151 @@
+"""GPU parity: libsage_mi355x (through the C ABI) against the CPU oracle.
+
+Integer work is bit-exact: K mean, Q/K codes and scales, V codes and scales,
+int32 QK^T accumulators.  Outputs are checked against the oracle's restatement
+of the reference's quantized attention with the stated tolerance
+(max-abs <= 2e-2, cosine >= 0.999), and against the oracle's emulation of the
+kernel's own P scaling with a tight tolerance.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import sage_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAXABS = 2e-2      # output max-abs vs the reference-scheme emulation
+TOL_COS = 0.999        # output cosine vs the reference-scheme emulation
+TIGHT_COS = 0.99999    # vs the emulation of the kernel's own P scaling
+TIGHT_MAXABS = 4e-3
+LSE_TOL = 2e-3         # log2 units
+
+
+def _sa():
+    from futudiffu_amd import sage_attention as SA
+    return SA
+
+
+def _bits(t):
+    t = t.contiguous()
+    if t.dtype in (torch.float32,):
+        return t.view(torch.int32)
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16)
+    if t.dtype == torch.float8_e4m3fn:
+        return t.view(torch.uint8)
+    return t
+
+
+def _assert_bits_equal(got, want, what):
+    g, w = _bits(got.cpu()), _bits(want.cpu())
+    assert g.shape == w.shape, f"{what}: shape {tuple(g.shape)} vs {tuple(w.shape)}"
+    bad = (g != w)
+    assert not bad.any(), f"{what}: {int(bad.sum())} of {bad.numel()} differ, first at {bad.nonzero()[0].tolist()}"
+
+
+QUANT_CASES = [
+    # (B, H, N, D, qk, pv, gran, smooth)
+    (1, 4, 256, 64, "int8", "bf16", "block64", True),
+    (1, 4, 256, 64, "int8", "bf16", "token", True),
+    (1, 2, 1280, 128, "int8", "fp8", "token", True),
+    (1, 2, 1280, 128, "fp8", "bf16", "token", True),
+    (1, 2, 1280, 128, "fp8", "fp8", "block64", True),
+    (2, 3, 200, 128, "int8", "fp8", "token", True),
+    (1, 2, 77, 64, "fp8", "fp8", "token", False),
+    (1, 1, 1, 128, "int8", "fp8", "token", True),
+]
+
+
+@pytest.mark.parametrize("B,H,N,D,qk,pv,gran,smooth", QUANT_CASES)
+def test_quantize_bitexact(cuda, B, H, N, D, qk, pv, gran, smooth):
+    from futudiffu_amd import layout
+    SA = _sa()
+    q, k, v = O.make_inputs(B, H, N, D, seed=N + D)
+    sm = 1.0 / math.sqrt(D)
+    qz = SA.quantize_qkv(q.to(cuda), k.to(cuda), v.to(cuda), sm, qk=qk, pv=pv, granularity=gran, smooth_k=smooth)
+    torch.cuda.synchronize()
+    oz = O.quantize_all(q, k, v, sm, qk, pv, gran, smooth)
+    BH, Np = B * H, qz.np_
+    if smooth:
+        _assert_bits_equal(qz.k_mean.view(B, H, 1, D), oz.mu, "k_mean")
+    codes_dt = torch.int8 if qk == "int8" else torch.float8_e4m3fn
+    for name, got, want in (("q_codes", qz.q_codes, oz.qc), ("k_codes", qz.k_codes, oz.kc)):
+        rows = layout.unpack_rows(got.cpu(), BH, Np, D)
+        _assert_bits_equal(rows[:, :N], want.contiguous().view(torch.uint8), name)
+        assert not rows[:, N:].any(), f"{name}: padded rows must be zero"
+        assert want.dtype == codes_dt
+    nsc = N if gran == "token" else (N + 63) // 64
+    _assert_bits_equal(qz.q_scale[:, :nsc], oz.qs, "q_scale")
+    _assert_bits_equal(qz.k_scale[:, :nsc], oz.ks, "k_scale")
+    if pv == "fp8":
+        vrows = layout.unpack_v_fp8(qz.v_op.cpu(), BH, Np, D)
+        _assert_bits_equal(vrows[:, :N], oz.vc.view(torch.uint8), "v_codes")
+        _assert_bits_equal(qz.v_scale[:, :(N + 63) // 64], oz.vs, "v_scale")
+    else:
+        vrows = layout.unpack_v_bf16(qz.v_op.cpu().view(torch.int16), BH, Np, D)
+        _assert_bits_equal(vrows[:, :N], v.reshape(BH, N, D).view(torch.int16), "v_bf16_fragments")
+
+
+@pytest.mark.parametrize("N,D", [(256, 64), (1280, 128), (200, 128), (33, 64)])
+def test_qk_int32_bitexact(cuda, N, D):
+    SA = _sa()
+    B, H = 1, 2
+    q, k, v = O.make_inputs(B, H, N, D, seed=7 + N)
+    qz = SA.quantize_qkv(q.to(cuda), k.to(cuda), v.to(cuda), qk="int8", pv="bf16")
+    s = SA.qk_int32(qz.q_codes, qz.k_codes, B * H, N, D)
+    torch.cuda.synchronize()
+    oz = O.quantize_all(q, k, v, 1.0 / math.sqrt(D), "int8", "bf16", "token", True)
+    want = O.qk_int32(oz.qc, oz.kc)
+    _assert_bits_equal(s[:, :N, :N], want, "qk_int32")
+
+
+def _compare(out, lse, q, k, v, qk, pv, gran, block_mask=None, doc_ids=None, smooth=True, tight=True):
+    ref, ref_lse, _ = O.sage_forward(q, k, v, None, qk, pv, gran, smooth, block_mask, doc_ids)
+    out = out.float().cpu()
+    lse = lse.cpu()
+    assert torch.isfinite(out).all(), "non-finite output"
+    maxabs = (out - ref.float()).abs().max().item()
+    cos = O.cosine(out, ref)
+    assert maxabs <= TOL_MAXABS, f"max-abs {maxabs:.4g} > {TOL_MAXABS} vs reference-scheme emulation"
+    assert cos >= TOL_COS, f"cosine {cos:.6f} < {TOL_COS} vs reference-scheme emulation"
+    fin = torch.isfinite(ref_lse)
+    assert torch.equal(fin, torch.isfinite(lse)), "LSE -inf pattern differs"
+    if fin.any():
+        lerr = (lse[fin] - ref_lse[fin]).abs().max().item()
+        assert lerr <= LSE_TOL, f"LSE error {lerr:.3g}"
+    if tight:
+        st, st_lse, _ = O.sage_forward(q, k, v, None, qk, pv, gran, smooth, block_mask, doc_ids,
+                                       p_scheme="static", tau=2.0)
+        tcos = O.cosine(out, st)
+        tmax = (out - st.float()).abs().max().item()
+        assert tcos >= TIGHT_COS, f"cosine {tcos:.7f} vs kernel-scheme emulation"
+        assert tmax <= TIGHT_MAXABS, f"max-abs {tmax:.4g} vs kernel-scheme emulation"
+    return maxabs, cos
+
+
+ATTN_CASES = [
+    (1, 4, 256, 64, "int8", "bf16", "block64"),
+    (1, 4, 256, 64, "int8", "bf16", "token"),
+    (1, 2, 1280, 128, "int8", "fp8", "token"),
+    (1, 2, 1280, 128, "int8", "bf16", "token"),
+    (1, 2, 1280, 128, "fp8", "bf16", "token"),
+    (1, 2, 1280, 128, "fp8", "fp8", "token"),
+    (1, 2, 1280, 128, "int8", "fp8", "block64"),
+    (2, 2, 200, 128, "int8", "fp8", "token"),
+    (1, 3, 77, 64, "fp8", "bf16", "token"),
+    (1, 2, 1, 128, "int8", "fp8", "token"),
+]
+
+
+@pytest.mark.parametrize("B,H,N,D,qk,pv,gran", ATTN_CASES)
+def test_attention_matches_oracle(cuda, B, H, N, D, qk, pv, gran):
+    SA = _sa()
+    q, k, v = O.make_inputs(B, H, N, D, seed=11 + N + D)
+    out, lse = SA.sage_forward(q.to(cuda), k.to(cuda), v.to(cuda), qk=qk, pv=pv, granularity=gran)
+    torch.cuda.synchronize()
+    assert out.shape == (B, H, N, D) and out.dtype == torch.bfloat16 and out.is_contiguous()
+    assert lse.shape == (B * H, N) and lse.dtype == torch.float32
+    _compare(out, lse, q, k, v, qk, pv, gran)
