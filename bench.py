@@ -1,0 +1,211 @@
+"""Benchmark of the MI355X Sage attention forward (one GPU).
+
+Workload: the headline shape B=1, H=30, N=4416, D=128 (1280x832 DiT image:
+4160 image tokens + 256 text tokens), bf16 q/k/v ~ N(0,1) with a per-channel
+K offset ~ N(0, 2), int8 QK (per-token scales) and fp8 P/V.  One "step" is one
+full op call: sage_quantize_qkv (smoothing + quantization) followed by
+sage_attn_fwd, with inputs resident in HBM.
+
+Prints ONE JSON line.  ``value`` is TFLOP/s of the whole op on the
+algorithmic count 4*B*H*N^2*D; ``roofline`` is the attention kernel (the
+dominant kernel) against the dense 8-bit MFMA peak; ``quantize`` reports the
+memory-bound kernel against HBM peak; ``cpu_baseline`` times the CPU oracle
+(the reference's algorithm restated in PyTorch) on a bounded sample of the
+same workload on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+PEAK_8BIT_TFLOPS = 5000.0   # MI355X dense fp8 / int8 MFMA, TFLOP/s (TOP/s)
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
+
+METRIC = "Sage attn fwd TFLOPS + ms/call at B=1,H=30,N=4416,D=128; % of fp8 MFMA peak"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--qk", default="int8", choices=["int8", "fp8"])
+    ap.add_argument("--pv", default="fp8", choices=["fp8", "bf16"])
+    ap.add_argument("--granularity", default="token", choices=["token", "block64"])
+    ap.add_argument("--B", type=int, default=1)
+    ap.add_argument("--H", type=int, default=30)
+    ap.add_argument("--N", type=int, default=4416)
+    ap.add_argument("--D", type=int, default=128)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU time budget of the cpu_baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def quant_bytes(B, H, N, D, pv, gran):
+    bh = B * H
+    rd = 3 * bh * N * D * 2
+    wr = 2 * bh * N * D + (bh * N * D if pv == "fp8" else 2 * bh * N * D)
+    nsc = N if gran == "token" else (N + 63) // 64
+    wr += 2 * bh * nsc * 4 + bh * D * 2
+    if pv == "fp8":
+        wr += bh * ((N + 63) // 64) * D * 4
+    return rd + wr
+
+
+def cpu_baseline(args, flop_per_head):
+    """Time the CPU oracle on whole heads of the same workload (bounded sample)."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import sage_oracle as O
+    threads = torch.get_num_threads()
+    q, k, v = O.make_inputs(1, 1, args.N, args.D, seed=123)
+    t0 = time.perf_counter()
+    O.sage_forward(q, k, v, None, args.qk, args.pv, args.granularity, True)
+    one = time.perf_counter() - t0
+    reps = max(1, min(8, int(args.cpu_seconds / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        O.sage_forward(q, k, v, None, args.qk, args.pv, args.granularity, True)
+    per_head = (time.perf_counter() - t0) / reps
+    t0 = time.perf_counter()
+    qf, kf, vf = q.float(), k.float(), v.float()
+    torch.nn.functional.scaled_dot_product_attention(q, k, v)
+    sdpa_head = time.perf_counter() - t0
+    return {
+        "value": round(flop_per_head / per_head / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle (torch CPU emulation of the reference quantized attention) on "
+                   f"{reps + 1} single-head runs B=1 H=1 N={args.N} D={args.D}; "
+                   f"{per_head * 1e3:.1f} ms/head, full call extrapolated x{args.B * args.H}"),
+        "ms_per_call_extrapolated": round(per_head * 1e3 * args.B * args.H, 3),
+        "sdpa_bf16_cpu_ms_per_head": round(sdpa_head * 1e3, 3),
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the forward shards by head with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from futudiffu_amd import sage_attention as SA
+
+    B, H, N, D = args.B, args.H, args.N, args.D
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q = torch.randn(B, H, N, D, generator=g).bfloat16().to(dev)
+    k = (torch.randn(B, H, N, D, generator=g) + 2.0 * torch.randn(B, H, 1, D, generator=g)).bfloat16().to(dev)
+    v = torch.randn(B, H, N, D, generator=g).bfloat16().to(dev)
+    sm = 1.0 / math.sqrt(D)
+    flop = 4.0 * B * H * N * N * D
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record()
+        qz = SA.quantize_qkv(q, k, v, sm, qk=args.qk, pv=args.pv, granularity=args.granularity)
+        if ev is not None:
+            ev[1].record()
+        out = SA.attn_from_quantized(qz, B, H)
+        if ev is not None:
+            ev[2].record()
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    qms = sorted(e[0].elapsed_time(e[1]) for e in evs)
+    ams = sorted(e[1].elapsed_time(e[2]) for e in evs)
+    ms_per_step = wall * 1e3 / args.steps
+    q_avg = sum(qms) / len(qms)
+    a_avg = sum(ams) / len(ams)
+
+    attn_tflops = flop / (a_avg * 1e-3) / 1e12
+    peak = PEAK_8BIT_TFLOPS
+    qbytes = quant_bytes(B, H, N, D, args.pv, args.granularity)
+    q_gbs = qbytes / (q_avg * 1e-3) / 1e9
+
+    res = {
+        "metric": METRIC,
+        "value": round(flop / (ms_per_step * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": f"{args.qk}-qk/{args.pv}-pv",
+        "data": "synthetic: q,k,v ~ N(0,1) bf16, K += N(0,2) per channel, seed 0",
+        "config": {
+            "workload": (f"sage_attn_fwd B={B} H={H} N={N} D={D} {args.qk}-QK {args.pv}-PV "
+                         f"{args.granularity} scales, no mask (quantize + fused attention)"),
+            "B": B, "H": H, "N": N, "D": D, "qk": args.qk, "pv": args.pv,
+            "granularity": args.granularity, "parallelism": "single GPU",
+        },
+        "pct_of_fp8_peak": round(100.0 * flop / (ms_per_step * 1e-3) / 1e12 / PEAK_8BIT_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "attn_fwd_kernel",
+            "achieved": round(attn_tflops, 3),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(attn_tflops / peak, 4),
+            "traffic": None,
+            "avg_kernel_ms": round(a_avg, 5),
+            "median_kernel_ms": round(ams[len(ams) // 2], 5),
+            "flop_per_launch": flop,
+        },
+        "quantize": {
+            "bound": "hbm",
+            "kernel": "k_colsum_kernel + quantize_kernel",
+            "achieved": round(q_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(q_gbs / PEAK_HBM_GBS, 4),
+            "algorithmic_bytes": qbytes,
+            "avg_ms": round(q_avg, 5),
+        },
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(args, flop / (B * H))
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()
