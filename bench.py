@@ -47,6 +47,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run a plain device copy of MIB MiB "
+                         "--steps times (scales the FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -105,6 +108,18 @@ def _cpu_model():
     return "unknown"
 
 
+def copy_calibration(args):
+    """Plain copy of a known size: the reference point for HBM byte counters."""
+    nbytes = args.copy_calibration << 20
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": nbytes, "copy_calibration_bytes_written": nbytes,
+                      "launches": args.steps}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -114,6 +129,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration(args)
+        return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from futudiffu_amd import sage_attention as SA
 

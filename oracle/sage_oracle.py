@@ -308,15 +308,15 @@ def attend(s: torch.Tensor, v: torch.Tensor, pv: str, visible: torch.Tensor | No
     Fully masked rows (no visible key) return 0 and ``lse = -inf`` (the
     reference would divide 0 by 0; its tile masks never produce such rows).
     """
-    bh, n, _ = s.shape
+    bh, n, nk = s.shape  # n queries, nk keys
     d = v.shape[-1]
     vfl = v.float()
     o = torch.zeros(bh, n, d)
     l = torch.zeros(bh, n, 1)
     m = torch.full((bh, n, 1), -math.inf)
     ninf = torch.tensor(-math.inf)
-    for j0 in range(0, n, BLOCK_N):
-        j1 = min(j0 + BLOCK_N, n)
+    for j0 in range(0, nk, BLOCK_N):
+        j1 = min(j0 + BLOCK_N, nk)
         sj = s[:, :, j0:j1]
         if visible is not None:
             sj = torch.where(visible[:, :, j0:j1], sj, ninf)

@@ -1,0 +1,154 @@
+"""The C ABI (include/sage_mi355x.h) and the host-side mirror, without a GPU.
+
+* libsage_mi355x.so loads and exports every function the header declares,
+  with the ctypes prototypes the Python glue binds.
+* Argument validation returns the documented status codes before any device
+  work (so no GPU is touched), with a message in sage_last_error().
+* The Python entry points raise the reference's exception types
+  (sage_attention.py:54-57 ValueError for bad variants, :487-488
+  AssertionError for head_dim/dtype).
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sage_mi355x.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\s*\*?\s+(sage_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declarations_found():
+    names = _declared()
+    assert {"sage_quantize_qkv", "sage_attn_fwd", "sage_abi_version", "sage_last_error"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol():
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes prototype"
+    assert lib.sage_abi_version() == 1
+
+
+def test_sizes_and_padding():
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    assert [lib.sage_padded_len(n) for n in (1, 128, 129, 4416)] == [128, 128, 256, 4480]
+    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 18 * 128 * 8
+    assert lib.sage_attn_workspace_bytes(2, 200) == 2 * (4 + 256 // 32) * 16
+
+
+def _quant_call(lib, **over):
+    a = dict(q=16, k=32, v=48, bh=2, n=100, d=128, qk=0, pv=1, gran=0, smooth=1, fold=0.18,
+             qc=64, qs=80, kc=96, ks=112, vo=128, vs=144, km=160, ws=176, wsb=1 << 20, stream=None)
+    a.update(over)
+    return lib.sage_quantize_qkv(a["q"], a["k"], a["v"], a["bh"], a["n"], a["d"], a["qk"], a["pv"], a["gran"],
+                                 a["smooth"], a["fold"], a["qc"], a["qs"], a["kc"], a["ks"], a["vo"], a["vs"],
+                                 a["km"], a["ws"], a["wsb"], a["stream"])
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(d=96), 1, "head_dim"),
+    (dict(n=0), 1, "positive"),
+    (dict(qk=3), 1, "qk_kind"),
+    (dict(pv=2), 1, "pv_kind"),
+    (dict(gran=7), 1, "granularity"),
+    (dict(q=None), 1, "null"),
+    (dict(vs=None), 1, "v_scale"),
+    (dict(k=33), 2, "aligned"),
+    (dict(km=None), 1, "k_mean"),
+    (dict(wsb=8), 3, "workspace"),
+    (dict(bh=70000), 1, "grid"),
+])
+def test_quantize_rejects_bad_arguments(over, status, msg):
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    assert _quant_call(lib, **over) == status
+    assert msg in lib.sage_last_error().decode()
+
+
+def _attn_call(lib, **over):
+    a = dict(qc=16, qs=32, kc=48, ks=64, vi=80, vs=96, b=1, h=2, n=300, d=128, qk=0, pv=1, gran=0,
+             mask=None, sz=0, nq=3, nkv=5, doc=None, ws=None, wsb=0, out=112, lse=128, stream=None)
+    a.update(over)
+    return lib.sage_attn_fwd(a["qc"], a["qs"], a["kc"], a["ks"], a["vi"], a["vs"], a["b"], a["h"], a["n"], a["d"],
+                             a["qk"], a["pv"], a["gran"], a["mask"], a["sz"], a["nq"], a["nkv"], a["doc"], a["ws"],
+                             a["wsb"], a["out"], a["lse"], a["stream"])
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(b=0), 1, "positive"),
+    (dict(d=64 + 32), 1, "head_dim"),
+    (dict(mask=256, nq=2), 1, "block_mask must be 3 x 5"),
+    (dict(mask=256, sz=7), 1, "mask_stride_z"),
+    (dict(doc=256, ws=None), 3, "workspace"),
+    (dict(doc=256, ws=264, wsb=1 << 20), 2, "workspace must be 16-byte aligned"),
+    (dict(out=None), 1, "null"),
+    (dict(pv=1, vs=None), 1, "v_scale"),
+])
+def test_attn_rejects_bad_arguments(over, status, msg):
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    assert _attn_call(lib, **over) == status
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_python_glue_error_types():
+    from futudiffu_amd import sage_attention as SA
+    q = torch.zeros(1, 2, 8, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        SA.sage_forward(q, q, q)
+    with pytest.raises(AssertionError, match="head_dim"):
+        x = torch.zeros(1, 2, 8, 96, dtype=torch.bfloat16)
+        SA.sage_forward(x, x, x)
+    with pytest.raises(AssertionError, match="BF16"):
+        x = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
+        SA.sage_forward(x, x, x)
+    with pytest.raises(ValueError, match="Unknown qk_quant"):
+        SA.configure_sage(qk_quant="int4")
+    with pytest.raises(ValueError, match="Unknown pv_quant"):
+        SA.configure_sage(pv_quant="fp16")
+    with pytest.raises(ValueError, match="must share one"):
+        SA.sage_forward(q, q[:, :1], q)
+
+
+def test_custom_op_schemas_and_fake_shapes():
+    import futudiffu_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    ops = torch.ops.futudiffu_ii
+    assert "block_mask" in str(ops.sage_attn_masked.default._schema)
+    with FakeTensorMode():
+        q = torch.empty(2, 3, 40, 128, dtype=torch.bfloat16)
+        m = torch.empty(1, 1, dtype=torch.uint8)
+        out, lse = ops.sage_attn_masked(q, q, q, m, 0.1)
+        assert out.shape == (2, 3, 40, 128) and out.dtype == torch.bfloat16
+        assert lse.shape == (6, 40) and lse.dtype == torch.float32
+        out, lse = ops.sage_attn(q, q, q, 0.1)
+        assert out.shape == (2, 3, 40, 128) and lse.shape == (6, 40)
+
+
+def test_layout_round_trip():
+    from futudiffu_amd import layout
+    x = torch.randint(0, 255, (3, 256, 128), dtype=torch.uint8)
+    assert torch.equal(layout.unpack_rows(layout.pack_rows(x), 3, 256, 128), x)
+    # every index map is a permutation
+    for fn in (layout._row_index, layout._v_fp8_index, layout._v_bf16_index):
+        idx = fn(256, 64)
+        assert torch.equal(idx.sort().values, torch.arange(256 * 64))
+
+
+def test_doc_id_builders():
+    from futudiffu_amd import block_mask as BM
+    d = BM.build_doc_ids([3, 2], total_len=7, device="cpu", batch=2)
+    assert d.tolist() == [[0, 0, 0, 1, 1, -1, -1]] * 2
+    v = torch.tensor([[True, False, True]])
+    assert BM.build_key_padding_doc_ids(v).tolist() == [[0, -1, 0]]

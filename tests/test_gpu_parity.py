@@ -149,3 +149,41 @@ def test_attention_matches_oracle(cuda, B, H, N, D, qk, pv, gran):
     assert out.shape == (B, H, N, D) and out.dtype == torch.bfloat16 and out.is_contiguous()
     assert lse.shape == (B * H, N) and lse.dtype == torch.float32
     _compare(out, lse, q, k, v, qk, pv, gran)
+
+
+def test_quantize_known_answers_at_ties(cuda):
+    """Rows whose amax makes the quantizer's multiplier exactly 1: the fp8 codes
+    of every e4m3 rounding tie (ties to even) and int8 truncation toward zero are
+    fixed by the formats, independent of any emulation."""
+    import numpy as np
+    from futudiffu_amd import layout
+    from oracle import np_codes as NC
+    SA = _sa()
+    D = 64
+    table = NC.e4m3_decode_table()
+    pos = np.sort(table[(~np.isnan(table)) & (table >= 0)])
+    ties = ((pos[:-1] + pos[1:]) / 2.0)
+    vals = np.concatenate([ties, -ties, [1.0, -2.5, 0.0]]).astype(np.float32)
+    per_row = D - 1
+    nrows = -(-len(vals) // per_row)
+    fp8_rows = np.zeros((nrows, D), np.float32)
+    fp8_rows[:, 0] = 448.0
+    fp8_rows.reshape(-1)[np.concatenate([np.arange(r * D + 1, (r + 1) * D) for r in range(nrows)])[:len(vals)]] = vals
+    int_vals = np.array([126.5, -126.5, 1.5, -1.5, 0.99, -0.99, 63.75, -0.25, 2.0, -2.0], np.float32)
+    int_rows = np.zeros((2, D), np.float32)
+    int_rows[:, 0] = 127.0
+    int_rows[0, 1:1 + len(int_vals)] = int_vals
+    for kind, rows in (("fp8", fp8_rows), ("int8", int_rows)):
+        n = rows.shape[0]
+        q = torch.from_numpy(rows).bfloat16().reshape(1, 1, n, D)
+        assert torch.equal(q.float().reshape(n, D), torch.from_numpy(rows)), "tie values must be exact in bf16"
+        qz = SA.quantize_qkv(q.to(cuda), q.to(cuda), q.to(cuda), 1.0, qk=kind, pv="bf16")
+        torch.cuda.synchronize()
+        codes = layout.unpack_rows(qz.q_codes.cpu(), 1, qz.np_, D)[0, :n].numpy()
+        if kind == "fp8":
+            want = NC.e4m3_encode(rows)
+        else:
+            want = np.trunc(rows).astype(np.int8).view(np.uint8)
+        assert np.array_equal(codes, want), f"{kind}: {np.argwhere(codes != want)[:5].tolist()}"
+        fold = float(np.float32(1.0 * 1.4426950408889634))
+        assert np.array_equal(qz.q_scale[0, :n].cpu().numpy(), np.full(n, np.float32(fold), np.float32))
