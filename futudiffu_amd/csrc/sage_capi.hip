@@ -116,7 +116,8 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
     mask |= 2;
     const int64_t nt = nkv;
     p.kv_sum = static_cast<const int4*>(workspace);
-    p.q_sum = static_cast<const int4*>(workspace) + b * nt;
+    p.q_sum = p.kv_sum + b * nt;
+    p.q_sum128 = p.q_sum + b * (sage::padded_len(n) / 32);
   }
   p.qc = static_cast<const uint8_t*>(q_codes);
   p.qs = q_scale;
@@ -133,8 +134,12 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
   p.n = n;
   p.np = sage::padded_len(n);
   p.h = (int)h;
+  p.bh = (int)(b * h);
   p.nt = (int)nkv;
-  hipError_t e = sage::launch_attn(qk_kind, pv_kind, granularity, mask, p, b * h, d, (int)b, stream);
+  p.light_last = (nq > 1 && n - (nq - 1) * 128 <= 64) ? 1 : 0;
+  if ((int64_t)p.bh * nq > 0x7fffffff)
+    return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(p.bh * nq));
+  hipError_t e = sage::launch_attn(qk_kind, pv_kind, granularity, mask, p, d, (int)b, stream);
   return launch_status(e, "sage_attn_fwd");
 }
 

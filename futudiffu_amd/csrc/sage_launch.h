@@ -18,13 +18,16 @@ struct AttnParams {
   int64_t mask_nkv;
   const int32_t* doc;
   const int4* kv_sum;  // [B][nT]   (min doc, max doc, #valid, #padding) over keys < N
-  const int4* q_sum;   // [B][Np/32] same over queries < N
+  const int4* q_sum;     // [B][Np/32] same over queries < N
+  const int4* q_sum128;  // [B][Np/128] same over queries < N
   uint16_t* out;
   float* lse;
   int64_t n;
   int64_t np;
-  int h;
-  int nt;
+  int h;           // heads per batch
+  int bh;          // B * H
+  int nt;          // key tiles: ceil(N / 64)
+  int light_last;  // last 128-row query tile holds <= 64 rows: schedule those items last
 };
 
 hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t* q, const uint16_t* k,
@@ -33,8 +36,7 @@ hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t
                            uint16_t* kmean, hipStream_t st);
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
 
-hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t bh, int64_t d, int nb,
-                       hipStream_t st);
+hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb, hipStream_t st);
 size_t attn_workspace_bytes(int64_t b, int64_t n);
 hipError_t launch_qk_int32(const uint8_t* qc, const uint8_t* kc, int64_t bh, int64_t n, int64_t d, int32_t* s,
                            hipStream_t st);

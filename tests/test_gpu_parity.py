@@ -117,8 +117,14 @@ def _compare(out, lse, q, k, v, qk, pv, gran, block_mask=None, doc_ids=None, smo
         lerr = (lse[fin] - ref_lse[fin]).abs().max().item()
         assert lerr <= LSE_TOL, f"LSE error {lerr:.3g}"
     if tight:
-        st, st_lse, _ = O.sage_forward(q, k, v, None, qk, pv, gran, smooth, block_mask, doc_ids,
-                                       p_scheme="static", tau=2.0)
+        # fp8 P: the kernel follows the reference per-(row, 64-key block) scaling, so the
+        # reference-scheme emulation is also the tight reference.  bf16 P: the kernel moves
+        # its reference point lazily (by more than 8 in log2 units), emulated exactly.
+        if pv == "fp8":
+            st = ref
+        else:
+            st, _, _ = O.sage_forward(q, k, v, None, qk, pv, gran, smooth, block_mask, doc_ids,
+                                      p_scheme="static", tau=8.0)
         tcos = O.cosine(out, st)
         tmax = (out - st.float()).abs().max().item()
         assert tcos >= TIGHT_COS, f"cosine {tcos:.7f} vs kernel-scheme emulation"
@@ -169,7 +175,7 @@ def test_quantize_known_answers_at_ties(cuda):
     fp8_rows = np.zeros((nrows, D), np.float32)
     fp8_rows[:, 0] = 448.0
     fp8_rows.reshape(-1)[np.concatenate([np.arange(r * D + 1, (r + 1) * D) for r in range(nrows)])[:len(vals)]] = vals
-    int_vals = np.array([126.5, -126.5, 1.5, -1.5, 0.99, -0.99, 63.75, -0.25, 2.0, -2.0], np.float32)
+    int_vals = np.array([126.5, -126.5, 1.5, -1.5, 0.9921875, -0.9921875, 63.75, -0.25, 2.0, -2.0], np.float32)
     int_rows = np.zeros((2, D), np.float32)
     int_rows[:, 0] = 127.0
     int_rows[0, 1:1 + len(int_vals)] = int_vals
@@ -187,3 +193,36 @@ def test_quantize_known_answers_at_ties(cuda):
         assert np.array_equal(codes, want), f"{kind}: {np.argwhere(codes != want)[:5].tolist()}"
         fold = float(np.float32(1.0 * 1.4426950408889634))
         assert np.array_equal(qz.q_scale[0, :n].cpu().numpy(), np.full(n, np.float32(fold), np.float32))
+
+
+MASK_CASES = [
+    # (B, H, N, D, qk, pv, kind)
+    (1, 2, 1023, 128, "int8", "fp8", "tile"),
+    (1, 2, 1023, 128, "int8", "bf16", "tile"),
+    (2, 2, 700, 128, "int8", "fp8", "doc"),
+    (2, 2, 700, 64, "fp8", "bf16", "doc"),
+    (1, 2, 1023, 128, "int8", "fp8", "tile+doc"),
+]
+
+
+@pytest.mark.parametrize("B,H,N,D,qk,pv,kind", MASK_CASES)
+def test_masked_attention_matches_oracle(cuda, B, H, N, D, qk, pv, kind):
+    SA = _sa()
+    q, k, v = O.make_inputs(B, H, N, D, seed=31 + N + D)
+    segs = [300, 500, 223]
+    bm = O.build_block_mask(segs, N) if "tile" in kind else None
+    doc = None
+    if "doc" in kind:
+        doc = torch.full((B, N), -1, dtype=torch.int32)
+        for b in range(B):
+            off = 0
+            for i, s in enumerate(segs if "tile" in kind else [250 - 40 * b, 300]):
+                doc[b, off:off + s] = i
+                off += s
+            doc[b, 20 + b:60 + b] = -1  # key padding inside the first segment
+    print(f"masked {kind} B={B} H={H} N={N} D={D} {qk}/{pv}", flush=True)
+    out, lse = SA.sage_forward(q.to(cuda), k.to(cuda), v.to(cuda), qk=qk, pv=pv,
+                               block_mask=None if bm is None else bm.to(cuda),
+                               doc_ids=None if doc is None else doc.to(cuda))
+    torch.cuda.synchronize()
+    _compare(out, lse, q, k, v, qk, pv, "token", block_mask=bm, doc_ids=doc)
