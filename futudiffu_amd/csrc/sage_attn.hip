@@ -8,36 +8,38 @@
 // Work decomposition: one workgroup = 4 waves = 128 query rows (the reference
 // Q tile, so a reference tile mask is workgroup-uniform); each wave owns 32
 // query rows.  Keys stream in 64-key tiles (the reference KV tile, which is
-// also the V-scale block).  K/V tiles are double-buffered in LDS: the global
-// loads of tile i+1 are issued into registers before tile i is computed and
-// written to the other LDS stage after it, with one barrier per tile.
+// also the V-scale block) through a ring of three LDS stages: while tile i is
+// consumed, tile i+1 already feeds the next S^T and tile i+2 travels from
+// global memory through registers into the third stage; one barrier per tile.
 //
 // Per wave and tile:
 //   S^T[key][query] = K . Q^T with v_mfma_i32_32x32x32_i8 (int8) or
 //   v_mfma_f32_32x32x64_f8f6f4 (fp8): lane (h, r) holds query r and keys
 //   32b + 8j + 4h + i, so every per-query reduction is lane-local (plus one
-//   permlane32 swap between the two lane halves).
+//   permlane32 swap between the two lane halves).  The S^T of tile i+1 is
+//   issued before the softmax of tile i so the matrix cores and the vector
+//   ALUs overlap within the wave.
 //   Online softmax in fp32 with exp2 (scores are in log2 units).
 //   O[query][d] += P . V with v_mfma_f32_32x32x64_f8f6f4 (fp8 P, fp8 V) or
 //   v_mfma_f32_32x32x16_bf16 (bf16 P, bf16 V).  P feeds the MFMA straight
 //   from the S^T registers: lane (h, r) already holds the keys its A operand
 //   needs.  O lane (h, r) holds channel 32c + r of rows 8j + 4h + i.
 //
+// O and l are kept in a lazily moved frame: they hold sums of 2^(s - m_ref),
+// where the per-row reference point m_ref only moves when a block max exceeds
+// it by more than kTau (then O and l are rescaled, which is rare after the
+// first tiles).  The LSE is m_ref + log2(l), the reference's m + log2(l).
 // fp8 P follows the reference per (row, 64-key block) scaling
-// (sage_kernels.py:1137-1141): with bm the block's row max and m the running
-// max, e = 2^(s - bm) * 448 is the code argument (= p * 448 / max(p) for
-// p = 2^(s - m)), and the block's PV product is dequantized by
-// 2^(bm - m) / 448 per row and the V scale per channel.
-// bf16 P uses a lazily moved reference point: p = 2^(s - m_ref) with m_ref
-// only raised when a block max exceeds it by more than kTauBf16; bf16 rounding
-// is relative, so this matches p = 2^(s - m) up to exp2 rounding while the O
-// rescale runs only on the rare tiles where m_ref moves.
+// (sage_kernels.py:1137-1141): with bm the block's row max, the code argument
+// is e = 2^(s - bm) * 448 (= p * 448 / max(p)), and the block's PV product is
+// dequantized by 2^(bm - m_ref) / 448 per row and the V scale per channel.
+// bf16 P is 2^(s - m_ref) rounded to bf16; bf16 rounding is relative, so this
+// matches the reference's bf16(2^(s - m)) up to exp2 rounding.
 #include "sage_common.h"
 #include "sage_launch.h"
 
 namespace sage {
 
-constexpr float kTauBf16 = 8.0f;
 constexpr float kLog2Fp8Max = 8.807354922057604f;  // log2(448)
 
 // Tile class for a block of queries against one key tile:
@@ -91,62 +93,269 @@ __global__ void doc_summary_kernel(const int32_t* __restrict__ doc, int64_t n, i
   *dst = make_int4(mn, mx, nv, ni);
 }
 
-// LDS stage layout (bytes): K codes, V operand, per-key K scales, per-channel
-// V scales, per-key document ids.
+// LDS stage layout (bytes): K codes, V operand, per-key K scales, per-key
+// additive score bias (-inf for keys past N), per-channel V scales, per-key
+// document ids.
 template <int D, int PV>
 struct Stage {
   static constexpr int kBytes = 64 * D;
   static constexpr int vBytes = (PV == kPV_FP8 ? 64 : 128) * D;
   static constexpr int offV = kBytes;
   static constexpr int offKd = offV + vBytes;
-  static constexpr int offVd = offKd + 256;
+  static constexpr int offKb = offKd + 256;  // per-key additive bias: 0, or -inf past N
+  static constexpr int offVd = offKb + 256;
   static constexpr int offDoc = offVd + 4 * D;
   static constexpr int bytes = offDoc + 256;
-  // 16-byte chunks per stage and where each group starts
+  // 16-byte chunks of the K|V bulk, spread over all 256 threads
   static constexpr int cK = kBytes / 16, cV = vBytes / 16;
-  static constexpr int cBulk = cK + cV;          // spread over all 256 threads
-  static constexpr int perThread = cBulk / 256;  // 4 (D=128 fp8), 6 (D=128 bf16), 2/3 (D=64)
+  static constexpr int perThread = (cK + cV) / 256;  // 4 (D=128 fp8), 6 (D=128 bf16), 2/3 (D=64)
 };
 
+// Workgroup LDS: a ring of three stages (tile i is consumed while tile i+1
+// feeds the next QK^T and tile i+2 is being written), then a 32-float row
+// exchange per wave.  The bf16 output staging of the epilogue reuses the ring.
 template <int D, int PV>
 struct Smem {
-  static constexpr int stages = 2 * Stage<D, PV>::bytes;
-  static constexpr int epilogue = 4 * 32 * D * 2;  // bf16 output staging, 4 waves x 32 rows
-  static constexpr int bytes = stages > epilogue ? stages : epilogue;
+  static constexpr int kStages = 3;
+  static constexpr int offX = kStages * Stage<D, PV>::bytes;
+  static constexpr int bytes = offX + 4 * 32 * 4;
+  static_assert(4 * 32 * D * 2 <= offX, "epilogue staging must fit in the stage ring");
 };
 
-// Work item of a workgroup.  Items are (bh, 128-row query tile); when the last
-// query tile of each head holds at most 64 rows (two idle waves), those light
-// items are ordered last so the final, partial dispatch round is short.
-__device__ __forceinline__ void item_of(int id, int bh_count, int nq, bool light_last, int& bh, int& qt) {
-  if (light_last && nq > 1) {
-    const int heavy = bh_count * (nq - 1);
-    if (id < heavy) {
-      bh = id / (nq - 1);
-      qt = id % (nq - 1);
-    } else {
-      bh = id - heavy;
-      qt = nq - 1;
+// Work item of a workgroup: (bh, 128-row query tile).
+// The hardware hands workgroup i to XCD i % 8, and each XCD has its own L2.
+// Items are therefore dealt to XCDs in contiguous head-major ranges, so the
+// workgroups resident on one XCD at a time cover about two heads and their
+// K/V tiles stay in that XCD's L2.  When the last query tile of each head
+// holds at most 64 rows (two idle waves), those light items come last in every
+// XCD's range so the final, partial dispatch round is short.
+__device__ __forceinline__ void item_of(int id, int total, int bh_count, int nq, bool light_last, int& bh, int& qt) {
+  constexpr int kXcd = 8;
+  const int light = (light_last && nq > 1) ? bh_count : 0;  // one light item per head
+  const int x = id % kXcd, local = id / kXcd;
+  const int per = total / kXcd, rem = total % kXcd;
+  const int lper = light / kXcd, lrem = light % kXcd;
+  const int count = per + (x < rem ? 1 : 0);
+  const int lcount = lper + (x < lrem ? 1 : 0);
+  const int lstart = x * lper + min(x, lrem);
+  const int hcount = count - lcount;
+  const int hstart = x * per + min(x, rem) - lstart;
+  const int nqh = light ? nq - 1 : nq;  // heavy tiles per head
+  if (local < hcount) {
+    const int hi = hstart + local;
+    bh = hi / nqh;
+    qt = hi % nqh;
+  } else {
+    bh = lstart + (local - hcount);
+    qt = nq - 1;
+  }
+}
+
+template <int QK>
+struct SAccT {
+  using type = f32x16;
+};
+template <>
+struct SAccT<kQK_INT8> {
+  using type = i32x16;
+};
+
+// One 32-key half b of the S^T tile for this wave's 32 queries: acc covers
+// keys 32b + (8j + 4h + i) in lane (h, r), element 4j + i.
+template <int D, int QK>
+__device__ __forceinline__ void qk_half(const uint8_t* sb, const i32x4* qf, int lane, int b,
+                                        typename SAccT<QK>::type& acc) {
+  constexpr int NC = D / 32;
+  const i32x4* kl = reinterpret_cast<const i32x4*>(sb);
+  if constexpr (QK == kQK_INT8) {
+    acc = i32x16{0};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(b * NC + c) * 64 + lane], qf[c], acc, 0, 0, 0);
+  } else {
+    acc = f32x16{0};
+#pragma unroll
+    for (int c = 0; c < NC; c += 2) {
+      const i32x8 bq = {qf[c][0], qf[c][1], qf[c][2], qf[c][3], qf[c + 1][0], qf[c + 1][1], qf[c + 1][2], qf[c + 1][3]};
+      const i32x4 a0 = kl[(b * NC + c) * 64 + lane], a1 = kl[(b * NC + c + 1) * 64 + lane];
+      const i32x8 ka = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka, bq, acc, 0, 0, 0, 0, 0, 0);
+    }
+  }
+}
+
+// Per-row values for the O fragment: lane (h, r) holds rows 8j + 4h + i,
+// element 4j + i.  Lanes h = 0 publish their row's value in the wave's
+// 32-float exchange; every lane then reads four broadcast float4s.
+__device__ __forceinline__ void rows_of(float* xrow, float v, int h, int r, float out[16]) {
+  if (h == 0) xrow[r] = v;
+  const f32x4* x4 = reinterpret_cast<const f32x4*>(xrow);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f32x4 q = x4[2 * j + h];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[4 * j + i] = q[i];
+  }
+}
+
+// The per-tile work of one wave, as straight-line code for the scheduler:
+// scores of tile t from s0/s1, the next tile's S^T into s0/s1 (issued early so
+// the matrix cores overlap this tile's vector work), online softmax, P.V.
+// MASKED selects the per-token document-id visibility test.
+template <int D, int QK, int PV, int GRAN, int MASK, bool MASKED>
+__device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_next, const i32x4* qf, int lane,
+                                          typename SAccT<QK>::type& s0, typename SAccT<QK>::type& s1, f32x16* o,
+                                          float& m_ref, float& l_acc, float wt, float* xrow, int dq) {
+  using St = Stage<D, PV>;
+  constexpr int NC = D / 32;
+  constexpr float kTau = 8.0f;  // lazy frame: the reference point moves when a block max exceeds it by this
+  const int h = lane >> 5, r = lane & 31;
+
+  // ---- scores of this tile: u = acc * kd + kbias (log2 units before wt) -------
+  // kd is the per-key K scale (the block scale for 64-token granularity) and
+  // kbias is -inf for keys past N, so the ragged last tile needs no test.
+  float u[2][16];
+  {
+    const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
+    const f32x4* kbl = reinterpret_cast<const f32x4*>(sb + St::offKb);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 kd4 = kdl[8 * b + 2 * j + h];
+        const f32x4 kb4 = kbl[8 * b + 2 * j + h];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) u[b][4 * j + i] = fmaf((float)(b ? s1 : s0)[4 * j + i], kd4[i], kb4[i]);
+      }
+  }
+  qk_half<D, QK>(sb_next, qf, lane, 0, s0);
+  if constexpr (MASKED) {
+    // per-token document ids: key visible iff doc[key] >= 0 and (doc[q] == doc[key] or doc[q] < 0)
+    const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int4 dk4 = dkl[8 * b + 2 * j + h];
+        const int dk[4] = {dk4.x, dk4.y, dk4.z, dk4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (!(dk[i] >= 0 && (dq == dk[i] || dq < 0))) u[b][4 * j + i] = -INFINITY;
+      }
+  }
+
+  // ---- row max: max3 tree, then across the two lane halves --------------------
+  float m4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    m4[k] = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(u[0][4 * k], u[0][4 * k + 1]), __builtin_fmaxf(u[0][4 * k + 2], u[0][4 * k + 3])),
+                            __builtin_fmaxf(__builtin_fmaxf(u[1][4 * k], u[1][4 * k + 1]), __builtin_fmaxf(u[1][4 * k + 2], u[1][4 * k + 3])));
+  float mx = __builtin_fmaxf(__builtin_fmaxf(m4[0], m4[1]), __builtin_fmaxf(m4[2], m4[3]));
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+  }
+  const float bm = mx * wt;  // -inf if nothing visible in this row
+  const bool row_live = bm > -INFINITY;
+
+  // ---- lazy frame move: values branch-free, the O rescale only when needed ---
+  const bool move = row_live && !(bm <= m_ref + kTau);
+  const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - bm) : 1.0f;  // 0 when m_ref = -inf
+  m_ref = move ? bm : m_ref;
+  l_acc *= alpha;
+  if (__any(move)) {
+    float arow[16];
+    rows_of(xrow, alpha, h, r, arow);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[c][e] *= arow[e];
+  }
+  qk_half<D, QK>(sb_next, qf, lane, 1, s1);
+
+  if constexpr (PV == kPV_FP8) {
+    // reference per-(row, 64-key block) P codes: e = 2^(s - bm) * 448; the
+    // block's product is dequantized by 2^(bm - m_ref) / 448 per row and by
+    // the V scale per channel (sage_kernels.py:1137-1153)
+    const float rsc = row_live ? __builtin_amdgcn_exp2f(bm - m_ref) * (1.0f / kFp8Max) : 0.0f;
+    const float bias = row_live ? (kLog2Fp8Max - bm) : 0.0f;  // masked u are -inf: e = 0
+    float es[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    i32x8 pa;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float e4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          e4[i] = __builtin_amdgcn_exp2f(fmaf(u[b][4 * j + i], wt, bias));
+          es[i] += e4[i];
+        }
+        pa[4 * b + j] = (int)pack_fp8x4(e4[0], e4[1], e4[2], e4[3]);
+      }
+    l_acc = fmaf(rsc, (es[0] + es[1]) + (es[2] + es[3]), l_acc);
+    float rrow[16];
+    rows_of(xrow, rsc, h, r, rrow);
+    const i32x4* vl = reinterpret_cast<const i32x4*>(sb + St::offV);
+    const float* vdl = reinterpret_cast<const float*>(sb + St::offVd);
+    f32x16 part[2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const i32x4 b0 = vl[(c * 2 + 0) * 64 + lane], b1 = vl[(c * 2 + 1) * 64 + lane];
+      const i32x8 bv = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+      part[c & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(pa, bv, f32x16{0}, 0, 0, 0, 0, 0, 0);
+      if (c >= 1) {
+        const float vd = vdl[32 * (c - 1) + r];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[c - 1][e] = fmaf(part[(c - 1) & 1][e], rrow[e] * vd, o[c - 1][e]);
+      }
+    }
+    {
+      const float vd = vdl[32 * (NC - 1) + r];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[NC - 1][e] = fmaf(part[(NC - 1) & 1][e], rrow[e] * vd, o[NC - 1][e]);
     }
   } else {
-    bh = id / nq;
-    qt = id % nq;
+    // bf16 P = 2^(s - m_ref) <= 2^kTau, accumulated straight into O
+    const float bias = row_live ? -m_ref : 0.0f;
+    float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 pa[2][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pr = __builtin_amdgcn_exp2f(fmaf(u[b][e], wt, bias));
+        ls[e & 3] += pr;
+        pa[b][e >> 3][e & 7] = (__bf16)pr;
+      }
+    l_acc += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    const bf16x8* vl = reinterpret_cast<const bf16x8*>(sb + St::offV);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[b][tt], vl[((c * 2 + b) * 2 + tt) * 64 + lane], o[c], 0, 0, 0);
   }
 }
 
 template <int D, int QK, int PV, int GRAN, int MASK>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   using St = Stage<D, PV>;
+  using SM = Smem<D, PV>;
+  using SAcc = typename SAccT<QK>::type;
   constexpr int NC = D / 32;  // 32-channel chunks
-  __shared__ __attribute__((aligned(16))) uint8_t smem[Smem<D, PV>::bytes];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SM::bytes];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, r = lane & 31;
   const int nq = (int)(p.np / kRowsPerWG);
   int bh, qt;
-  item_of(blockIdx.x, p.bh, nq, p.light_last, bh, qt);
+  item_of(blockIdx.x, (int)gridDim.x, p.bh, nq, p.light_last, bh, qt);
   const int bidx = bh / p.h;
   const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * wave;  // first query row of this wave
   const bool wave_live = q0 < p.n;
+  float* xrow = reinterpret_cast<float*>(smem + SM::offX) + 32 * wave;
 
   // ---- per-wave query state ------------------------------------------------
   i32x4 qf[NC];
@@ -171,7 +380,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
     qsum128 = p.q_sum128[(int64_t)bidx * nq + qt];
   }
 
-  float m_run = -INFINITY;  // fp8 PV: running row max; bf16 PV: lazy reference point
+  // Row state in a lazily moved frame: O and l hold sums of 2^(s - m_ref).
+  float m_ref = -INFINITY;
   float l_acc = 0.0f;
   f32x16 o[NC];
 #pragma unroll
@@ -182,27 +392,26 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   const int32_t* docb = (MASK & 2) ? p.doc + (int64_t)bidx * p.n : nullptr;
 
   // ---- tile schedule: active tiles in order ----------------------------------
-  auto active = [&](int t) -> bool {
-    if (MASK & 1) {
-      if (p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] == 0) return false;
-    }
-    if (MASK & 2) {
-      if (classify(qsum128, p.kv_sum[(int64_t)bidx * p.nt + t]) == 0) return false;
-    }
-    return true;
-  };
   auto next_active = [&](int t) -> int {
-    while (t < p.nt && !active(t)) ++t;
+    for (; t < p.nt; ++t) {
+      if (MASK & 1) {
+        if (p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] == 0) continue;
+      }
+      if (MASK & 2) {
+        if (classify(qsum128, p.kv_sum[(int64_t)bidx * p.nt + t]) == 0) continue;
+      }
+      break;
+    }
     return t;
   };
 
   // ---- loads: global -> registers -> LDS stage ---------------------------------
   // Thread tid moves 16-byte chunks tid + 256*i of the stage's K|V bulk, and
-  // threads 0..63 one small chunk: K scales (0..15), V scales (16..16+D/4),
-  // key document ids (48..63).
+  // threads 0..63 one small chunk: K scales and score biases (0..15), V scales
+  // (16..16+D/4), key document ids (48..63).
   static_assert(St::perThread <= 6 && St::cK % 256 == 0, "stage chunking");
   uint4 pre0, pre1, pre2, pre3, pre4, pre5;  // scalars: an indexed array would live in scratch
-  uint4 pre_small = make_uint4(0, 0, 0, 0);
+  uint4 pre_small = make_uint4(0, 0, 0, 0), pre_bias = make_uint4(0, 0, 0, 0);
 #define SAGE_CHUNK_LD(I_, DST_)                                                                        \
   if constexpr (St::perThread > I_) DST_ = (256 * I_ < St::cK) ? ksrc_[tid + 256 * I_] : vsrc_[tid + 256 * I_ - St::cK]
 #define SAGE_CHUNK_ST(I_, SRC_) \
@@ -211,6 +420,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   do {                                                                                                 \
     const uint4* ksrc_ = reinterpret_cast<const uint4*>(kg + (int64_t)(T_) * 64 * D);                  \
     const uint4* vsrc_ = reinterpret_cast<const uint4*>(vg + (int64_t)(T_) * St::vBytes);              \
+    const uint32_t kdb_ = GRAN == kGRAN_TOKEN ? 0u : __float_as_uint(p.ks[(int64_t)bh * (p.np / 64) + (T_)]); \
     SAGE_CHUNK_LD(0, pre0);                                                                            \
     SAGE_CHUNK_LD(1, pre1);                                                                            \
     SAGE_CHUNK_LD(2, pre2);                                                                            \
@@ -220,6 +430,12 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
     if (tid < 16) {                                                                                    \
       if (GRAN == kGRAN_TOKEN)                                                                         \
         pre_small = reinterpret_cast<const uint4*>(p.ks + (int64_t)bh * p.np + (int64_t)(T_) * 64)[tid]; \
+      else                                                                                             \
+        pre_small = make_uint4(kdb_, kdb_, kdb_, kdb_);                                                \
+      const int key_ = (T_) * 64 + 4 * tid;                                                            \
+      const uint32_t ninf_ = 0xff800000u;                                                              \
+      pre_bias = make_uint4(key_ + 0 < p.n ? 0u : ninf_, key_ + 1 < p.n ? 0u : ninf_,                  \
+                            key_ + 2 < p.n ? 0u : ninf_, key_ + 3 < p.n ? 0u : ninf_);                 \
     } else if (tid < 16 + D / 4) {                                                                     \
       if (PV == kPV_FP8)                                                                               \
         pre_small = reinterpret_cast<const uint4*>(p.vs + ((int64_t)bh * (p.np / 64) + (T_)) * D)[tid - 16]; \
@@ -241,7 +457,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
     SAGE_CHUNK_ST(4, pre4);                                                                            \
     SAGE_CHUNK_ST(5, pre5);                                                                            \
     if (tid < 16) {                                                                                    \
-      if (GRAN == kGRAN_TOKEN) reinterpret_cast<uint4*>(sb_ + St::offKd)[tid] = pre_small;             \
+      reinterpret_cast<uint4*>(sb_ + St::offKd)[tid] = pre_small;                                      \
+      reinterpret_cast<uint4*>(sb_ + St::offKb)[tid] = pre_bias;                                       \
     } else if (tid < 16 + D / 4) {                                                                     \
       if (PV == kPV_FP8) reinterpret_cast<uint4*>(sb_ + St::offVd)[tid - 16] = pre_small;              \
     } else if ((MASK & 2) && tid >= 48 && tid < 64) {                                                  \
@@ -249,217 +466,75 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
     }                                                                                                  \
   } while (0)
 
+  // ---- prologue: tiles 0 and 1 of the schedule in stages 0 and 1 --------------
   int t = next_active(0);
+  int t1 = t < p.nt ? next_active(t + 1) : p.nt;
+  int t2 = t1 < p.nt ? next_active(t1 + 1) : p.nt;
   if (t < p.nt) {
     SAGE_LOAD_TILE(t);
     SAGE_STORE_TILE(0);
   }
+  if (t1 < p.nt) {
+    SAGE_LOAD_TILE(t1);
+    SAGE_STORE_TILE(1);
+  }
   __syncthreads();
+  SAcc s0, s1;  // S^T of the tile about to be consumed
+  if (t < p.nt && wave_live) {
+    qk_half<D, QK>(smem, qf, lane, 0, s0);
+    qk_half<D, QK>(smem, qf, lane, 1, s1);
+  }
+
   int stage = 0;
   while (t < p.nt) {
-    const int tn = next_active(t + 1);
-    if (tn < p.nt) SAGE_LOAD_TILE(tn);
+    if (t2 < p.nt) SAGE_LOAD_TILE(t2);
     const uint8_t* sb = smem + stage * St::bytes;
+    const int stage1 = stage == 2 ? 0 : stage + 1;
+    const int stage2 = stage1 == 2 ? 0 : stage1 + 1;
+    // the last tile recomputes its own S^T in place of a next tile's (unused)
+    const uint8_t* sb_next = t1 < p.nt ? smem + stage1 * St::bytes : sb;
 
     int cls = wave_live ? 1 : 0;
     if ((MASK & 2) && cls) cls = classify(qsum, p.kv_sum[(int64_t)bidx * p.nt + t]);
-    if (cls) {
-      const bool oob = (int64_t)(t + 1) * 64 > p.n;
-      const bool elem_mask = oob || cls == 2;
-
-      // ---- S^T = K . Q^T ------------------------------------------------------
-      float u[2][16];
-      const i32x4* kl = reinterpret_cast<const i32x4*>(sb);
-      if (QK == kQK_INT8) {
-        i32x16 acc0 = i32x16{0}, acc1 = i32x16{0};
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(0 * NC + c) * 64 + lane], qf[c], acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(1 * NC + c) * 64 + lane], qf[c], acc1, 0, 0, 0);
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          u[0][e] = (float)acc0[e];
-          u[1][e] = (float)acc1[e];
-        }
-      } else {
-        f32x16 acc0 = f32x16{0}, acc1 = f32x16{0};
-#pragma unroll
-        for (int c = 0; c < NC; c += 2) {
-          const i32x8 bq = {qf[c][0], qf[c][1], qf[c][2], qf[c][3],
-                            qf[c + 1][0], qf[c + 1][1], qf[c + 1][2], qf[c + 1][3]};
-          const i32x4 a0 = kl[(0 * NC + c) * 64 + lane], a1 = kl[(0 * NC + c + 1) * 64 + lane];
-          const i32x4 b0 = kl[(1 * NC + c) * 64 + lane], b1 = kl[(1 * NC + c + 1) * 64 + lane];
-          const i32x8 ka = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-          const i32x8 kb = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-          acc0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka, bq, acc0, 0, 0, 0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kb, bq, acc1, 0, 0, 0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          u[0][e] = acc0[e];
-          u[1][e] = acc1[e];
-        }
-      }
-
-      // ---- per-key scale, masks -------------------------------------------------
-      float wt = w;  // multiplier taking u to log2-domain scores
-      if (GRAN == kGRAN_TOKEN) {
-        const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const f32x4 kd4 = kdl[8 * b + 2 * j + h];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) u[b][4 * j + i] *= kd4[i];
-          }
-      } else {
-        wt = fmaxf(qd * p.ks[(int64_t)bh * (p.np / 64) + t], 1e-30f);
-      }
-      if (elem_mask) {
-        const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            int4 dk4 = make_int4(0, 0, 0, 0);
-            if ((MASK & 2) && cls == 2) dk4 = dkl[8 * b + 2 * j + h];
-            const int dk[4] = {dk4.x, dk4.y, dk4.z, dk4.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int64_t key = (int64_t)t * 64 + 32 * b + 8 * j + 4 * h + i;
-              bool vis = key < p.n;
-              if ((MASK & 2) && cls == 2) vis = vis && dk[i] >= 0 && (dq == dk[i] || dq < 0);
-              if (!vis) u[b][4 * j + i] = -INFINITY;
-            }
-          }
-      }
-
-      // ---- row max of this tile (log2 units) ----------------------------------
-      float mx = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, u[b][e]);
-      {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      }
-      const float bm = mx * wt;  // -inf if nothing visible in this row
-
-      if (PV == kPV_FP8) {
-        // reference per-(row, 64-key block) P scaling
-        const float m_new = fmaxf(m_run, bm);
-        const bool row_live = bm > -INFINITY;  // some key of this tile is visible to the row
-        const float alpha = m_new > -INFINITY ? exp2f(m_run - m_new) : 1.0f;  // 0 on the first live tile
-        const float rsc = row_live ? exp2f(bm - m_new) * (1.0f / kFp8Max) : 0.0f;
-        const float bias = row_live ? (kLog2Fp8Max - bm) : 0.0f;  // masked u are -inf: e = 0
-        m_run = m_new;
-        float esum = 0.0f;
-        i32x8 pa;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float e4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              e4[i] = __builtin_amdgcn_exp2f(fmaf(u[b][4 * j + i], wt, bias));
-              esum += e4[i];
-            }
-            pa[4 * b + j] = (int)pack_fp8x4(e4[0], e4[1], e4[2], e4[3]);
-          }
-        l_acc = fmaf(l_acc, alpha, rsc * esum);
-        // per-row factors for the O fragment rows 8j + 4h + i
-        const bool any_move = __any(alpha != 1.0f);
-        float rrow[16], arow[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) rrow[e] = __shfl(rsc, 8 * (e >> 2) + 4 * h + (e & 3));
-        if (any_move) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) arow[e] = __shfl(alpha, 8 * (e >> 2) + 4 * h + (e & 3));
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) o[c][e] *= arow[e];
-        }
-        const i32x4* vl = reinterpret_cast<const i32x4*>(sb + St::offV);
-        const float* vdl = reinterpret_cast<const float*>(sb + St::offVd);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const i32x4 b0 = vl[(c * 2 + 0) * 64 + lane], b1 = vl[(c * 2 + 1) * 64 + lane];
-          const i32x8 bv = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-          const f32x16 part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(pa, bv, f32x16{0}, 0, 0, 0, 0, 0, 0);
-          const float vd = vdl[32 * c + r];
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[c][e] = fmaf(part[e], rrow[e] * vd, o[c][e]);
-        }
-      } else {
-        // lazily moved reference point, bf16 P
-        const bool move = (bm > m_run + kTauBf16) || (m_run == -INFINITY && bm > -INFINITY);
-        float alpha = 1.0f;
-        if (move) {
-          alpha = exp2f(m_run - bm);  // 0 when m_run = -inf
-          m_run = bm;
-          l_acc *= alpha;
-        }
-        if (__any(move)) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const float a = __shfl(alpha, 8 * (e >> 2) + 4 * h + (e & 3));
-#pragma unroll
-            for (int c = 0; c < NC; ++c) o[c][e] *= a;
-          }
-        }
-        const float bias = (m_run == -INFINITY) ? 0.0f : -m_run;
-        bf16x8 pa[2][2];
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const float pr = __builtin_amdgcn_exp2f(fmaf(u[b][e], wt, bias));
-            l_acc += pr;
-            pa[b][e >> 3][e & 7] = (__bf16)pr;
-          }
-        const bf16x8* vl = reinterpret_cast<const bf16x8*>(sb + St::offV);
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-              o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[b][tt], vl[((c * 2 + b) * 2 + tt) * 64 + lane], o[c],
-                                                             0, 0, 0);
-      }
+    if (cls == 2)
+      tile_body<D, QK, PV, GRAN, MASK, true>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq);
+    else if (cls == 1)
+      tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq);
+    else if (wave_live && t1 < p.nt) {
+      qk_half<D, QK>(sb_next, qf, lane, 0, s0);
+      qk_half<D, QK>(sb_next, qf, lane, 1, s1);
     }
 
-    // ---- hand over to the next tile -------------------------------------------
-    if (tn < p.nt) SAGE_STORE_TILE(stage ^ 1);
+    // ---- hand over: tile t2 into the stage tile t - 1 used ----------------------
+    if (t2 < p.nt) SAGE_STORE_TILE(stage2);
     __syncthreads();
-    stage ^= 1;
-    t = tn;
+    stage = stage1;
+    t = t1;
+    t1 = t2;
+    t2 = t2 < p.nt ? next_active(t2 + 1) : p.nt;
   }
-
 #undef SAGE_LOAD_TILE
 #undef SAGE_STORE_TILE
 #undef SAGE_CHUNK_LD
 #undef SAGE_CHUNK_ST
 
   // ---- epilogue: LSE, normalize, stage bf16 rows in LDS, 16-byte stores --------
-  const float l_tot = l_acc + __shfl_xor(l_acc, 32);
-  const bool empty = !(l_tot > 0.0f);
-  const float inv_l = empty ? 0.0f : 1.0f / l_tot;
-  if (wave_live && h == 0 && q0 + r < p.n)
-    p.lse[(int64_t)bh * p.n + q0 + r] = empty ? -INFINITY : (m_run + log2f(l_tot));
   if (!wave_live) return;  // no barrier follows
+  float l_tot;
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_acc), __float_as_uint(l_acc), false, false);
+    l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  const bool empty = !(l_tot > 0.0f);
+  if (h == 0 && q0 + r < p.n) p.lse[(int64_t)bh * p.n + q0 + r] = empty ? -INFINITY : (m_ref + log2f(l_tot));
+  float srow[16];
+  rows_of(xrow, empty ? 0.0f : 1.0f / l_tot, h, r, srow);
   uint16_t* ep = reinterpret_cast<uint16_t*>(smem) + wave * 32 * D;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int row = 8 * (e >> 2) + 4 * h + (e & 3);
-    const float s = __shfl(inv_l, row);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) ep[row * D + 32 * c + r] = f32_to_bf16_rne(o[c][e] * s);
+    for (int c = 0; c < NC; ++c) ep[row * D + 32 * c + r] = f32_to_bf16_rne(o[c][e] * srow[e]);
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
   __builtin_amdgcn_wave_barrier();
