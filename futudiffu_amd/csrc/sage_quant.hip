@@ -9,111 +9,65 @@
 // The reference re-quantizes K for every 128-row Q tile inside the attention
 // loop; per-token scales depend only on the token, so quantizing once here
 // yields identical codes.
+//
+// quantize (one workgroup per 64-token block and head) issues all of its Q,
+// K and V loads up front, writes Q and V codes and adds the block's fp64 K
+// column sums into per-head sums (zeroed just before by k_sum_zero).
+// k_quantize then forms each head's mean and writes the K codes; it is the
+// only second read of K, which the mean makes unavoidable (every K code
+// depends on all N tokens).  Without smoothing, quantize writes the K codes
+// itself.
 #include "sage_common.h"
 #include "sage_launch.h"
 
 namespace sage {
 
-constexpr int kSumChunk = 256;  // tokens per partial K column sum
-
-// Pass 1: fp64 partial column sums of K per (bh, 256-token chunk).
-// The sum of bf16 values in fp64 is exact for realistic inputs, so the mean
-// does not depend on the order the chunks are combined in.
-template <int D>
-__global__ void __launch_bounds__(256) k_colsum_kernel(const uint16_t* __restrict__ k, int64_t n,
-                                                       double* __restrict__ ws, int nchunks) {
-  constexpr int LPR = D / 8;       // lanes per token row (8 channels each)
-  constexpr int RPP = 256 / LPR;   // rows per pass
-  __shared__ double red[RPP * D];
-  const int bh = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x;
-  const int c8 = tid % LPR, rr = tid / LPR;
-  const uint16_t* kb = k + (int64_t)bh * n * D;
-  double acc[8];
+// 8 bf16 (one 16-byte load) -> fp32.
+__device__ __forceinline__ void unpack8(uint4 w, float x[8]) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0;
-  const int64_t r0 = (int64_t)chunk * kSumChunk;
-  const int64_t r1 = r0 + kSumChunk < n ? r0 + kSumChunk : n;
-  for (int64_t r = r0 + rr; r < r1; r += RPP) {
-    const uint4 w = *reinterpret_cast<const uint4*>(kb + r * D + c8 * 8);
-    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc[2 * e] += (double)bf16_to_f32((uint16_t)(ww[e] & 0xffffu));
-      acc[2 * e + 1] += (double)bf16_to_f32((uint16_t)(ww[e] >> 16));
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) red[rr * D + c8 * 8 + e] = acc[e];
-  __syncthreads();
-  if (tid < D) {
-    double s = 0.0;
-    for (int i = 0; i < RPP; ++i) s += red[i * D + tid];
-    ws[((int64_t)bh * nchunks + chunk) * D + tid] = s;
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = __uint_as_float(ww[e] << 16);
+    x[2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
   }
 }
 
-// Load 8 bf16 channels [8*c8, 8*c8+8) of token `tok` as fp32 (zeros past n).
-template <int D>
-__device__ __forceinline__ void load8(const uint16_t* __restrict__ base, int64_t tok, int64_t n, int c8,
-                                      float x[8]) {
-  if (tok < n) {
-    const uint4 w = *reinterpret_cast<const uint4*>(base + tok * D + c8 * 8);
-    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x[2 * e] = bf16_to_f32((uint16_t)(ww[e] & 0xffffu));
-      x[2 * e + 1] = bf16_to_f32((uint16_t)(ww[e] >> 16));
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-  }
+// Max over aligned groups of G lanes (G in {8, 16}) with DPP row permutes:
+// quad xor 1, quad xor 2, half-row mirror (8 lanes), row mirror (16 lanes).
+template <int G>
+__device__ __forceinline__ float group_max(float a) {
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xf, 0xf, false)));  // [1,0,3,2]
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xf, 0xf, false)));  // [2,3,0,1]
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x141, 0xf, 0xf, false)));  // half mirror
+  if constexpr (G == 16) a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x140, 0xf, 0xf, false)));
+  return a;
 }
 
-// Quantize one operand (Q or K) for the 64 tokens of this workgroup and write
-// codes in row-fragment order plus scales.
-template <int D, int QK, int GRAN, bool SMOOTH>
-__device__ __forceinline__ void quantize_rows(const uint16_t* __restrict__ src, int64_t n, int64_t np,
-                                              int64_t tok0, const float* mu, float fold,
-                                              uint8_t* __restrict__ codes, float* __restrict__ scale,
-                                              unsigned int* blk_amax_u) {
-  constexpr int LPR = D / 8;
-  constexpr int RPP = 256 / LPR;
-  constexpr int PASSES = 64 / RPP;
-  const int tid = threadIdx.x, c8 = tid % LPR, rr = tid / LPR;
+// Max across the 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float rows_max(float a) {
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+  a = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+  return fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+}
+
+__device__ __forceinline__ uint32_t word_of(uint4 w, int i) {
+  return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
+}
+
+// Quantize the 8 channels a lane holds for each of its PASSES tokens of one
+// operand (Q or K) and store codes in row-fragment order plus scales.
+// x holds the (smoothed) values; amax is per token, or per 64-token block.
+template <int D, int QK, int GRAN, int PASSES>
+__device__ __forceinline__ void store_rows(const float (&x)[PASSES][8], const float (&amax)[PASSES], int64_t tok0,
+                                           int rr, int c8, float fold, uint8_t* __restrict__ codes,
+                                           float* __restrict__ scale, int tid) {
+  constexpr int RPP = 256 / (D / 8);
   const float qmax = (QK == kQK_INT8) ? kInt8Max : kFp8Max;
-  float x[PASSES][8];
-  float ramax[PASSES];
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
     const int64_t tok = tok0 + rr + ps * RPP;
-    load8<D>(src, tok, n, c8, x[ps]);
-    if (SMOOTH && tok < n) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[ps][e] = bf16_to_f32(f32_to_bf16_rne(x[ps][e] - mu[c8 * 8 + e]));
-    }
-    float a = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(x[ps][e]));
-#pragma unroll
-    for (int off = 1; off < LPR; off <<= 1) a = fmaxf(a, __shfl_xor(a, off, LPR));
-    ramax[ps] = a;
-  }
-  if (GRAN == kGRAN_BLOCK64) {
-    float a = 0.0f;
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) a = fmaxf(a, ramax[ps]);
-    if (c8 == 0) atomicMax(blk_amax_u, __float_as_uint(a));
-    __syncthreads();
-    a = __uint_as_float(*blk_amax_u);
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) ramax[ps] = a;
-  }
-#pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) {
-    const int64_t tok = tok0 + rr + ps * RPP;
-    const float amax = ramax[ps];
-    const float inv = qmax / fmaxf(amax, kEps);  // IEEE division (correctly rounded)
+    const float inv = qmax / fmaxf(amax[ps], kEps);  // IEEE division (correctly rounded)
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = x[ps][e] * inv;
@@ -126,123 +80,272 @@ __device__ __forceinline__ void quantize_rows(const uint16_t* __restrict__ src, 
       word.y = pack_fp8x4(y[4], y[5], y[6], y[7]);
     }
     const int d0 = c8 * 8;
-    const int64_t off = row_frag_offset(tok, d0 / 32, (d0 / 16) & 1, D) + (d0 & 8);
-    *reinterpret_cast<uint2*>(codes + off) = word;
+    *reinterpret_cast<uint2*>(codes + row_frag_offset(tok, d0 / 32, (d0 / 16) & 1, D) + (d0 & 8)) = word;
     if (GRAN == kGRAN_TOKEN) {
-      if (c8 == 0) scale[tok] = (amax / qmax) * fold;
+      if (c8 == 0) scale[tok] = (amax[ps] / qmax) * fold;
     } else if (tid == 0 && ps == 0) {
-      scale[tok0 / 64] = (amax / qmax) * fold;
+      scale[tok0 / 64] = (amax[ps] / qmax) * fold;
     }
   }
 }
 
+// Per-token (or per-block) |x| maxima of a lane's tokens.
+template <int D, int GRAN, int PASSES>
+__device__ __forceinline__ void row_amax(const float (&x)[PASSES][8], float (&amax)[PASSES], unsigned int* blk_u) {
+  constexpr int LPR = D / 8;
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    float a = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(x[ps][e]));
+    amax[ps] = group_max<LPR>(a);
+  }
+  if (GRAN == kGRAN_BLOCK64) {
+    float a = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) a = fmaxf(a, amax[ps]);
+    if ((threadIdx.x % LPR) == 0) atomicMax(blk_u, __float_as_uint(a));
+    __syncthreads();
+    a = __uint_as_float(*blk_u);
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) amax[ps] = a;
+  }
+}
+
 // Pass 2: one workgroup per (64-token block, bh).
+//   Q, K: lane (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps.
+//   V:    lane (g, c8) holds channels [8*c8, +8) of the 4 consecutive tokens
+//         4g..4g+3, so the 4 codes of a channel form one 32-bit fragment word.
 template <int D, int QK, int PV, int GRAN, bool SMOOTH>
 __global__ void __launch_bounds__(256) quantize_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    int64_t n, int64_t np, float fold, const double* __restrict__ ws, int nchunks,
+    int64_t n, int64_t np, float fold, double* __restrict__ ksum,
     uint8_t* __restrict__ qc, float* __restrict__ qs, uint8_t* __restrict__ kc, float* __restrict__ ks,
-    uint8_t* __restrict__ vout, float* __restrict__ vs, uint16_t* __restrict__ kmean) {
+    uint8_t* __restrict__ vout, float* __restrict__ vs) {
+  constexpr int LPR = D / 8;
+  constexpr int RPP = 256 / LPR;
+  constexpr int PASSES = 64 / RPP;
+  constexpr int VTHREADS = 16 * LPR;  // 16 groups of 4 tokens
+  __shared__ unsigned int blk_amax[2];
+  __shared__ __attribute__((aligned(16))) float vmax[4][D];
+  __shared__ double ksw[SMOOTH ? 4 : 1][D];
+  // V operand image of this 64-token block in fragment order; written to
+  // global as contiguous 16-byte chunks
+  __shared__ __attribute__((aligned(16))) uint8_t vimg[(PV == kPV_FP8 ? 1 : 2) * 64 * D];
+  const int bh = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
+  const int c8 = tid % LPR, rr = tid / LPR;
+  const int64_t tok0 = (int64_t)blk * 64;
+  const int64_t so = (int64_t)bh * n * D;
+  const int64_t co = (int64_t)bh * np * D;
+  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+
+  if (tid < 2) blk_amax[tid] = 0u;
+  __syncthreads();
+
+  // ---- issue every load of the block up front ------------------------------
+  // Token indices are clamped to N-1 so every load is in bounds and issued
+  // without branches; values of tokens past N are zeroed afterwards.
+  uint4 qw[PASSES], kw[PASSES], vw[4];
+  const uint4 zero4 = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int64_t tok = min(tok0 + rr + ps * RPP, n - 1);
+    qw[ps] = *reinterpret_cast<const uint4*>(q + so + tok * D + c8 * 8);
+    kw[ps] = *reinterpret_cast<const uint4*>(k + so + tok * D + c8 * 8);
+  }
+  const int g = (tid / LPR) & 15;  // V token group (V work only for tid < VTHREADS)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t tok = min(tok0 + 4 * g + i, n - 1);
+    vw[i] = *reinterpret_cast<const uint4*>(v + so + tok * D + c8 * 8);
+  }
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    if (tok0 + rr + ps * RPP >= n) {
+      qw[ps] = zero4;
+      kw[ps] = zero4;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (tid >= VTHREADS || tok0 + 4 * g + i >= n) vw[i] = zero4;
+  // ---- Q -----------------------------------------------------------------------
+  {
+    float x[PASSES][8], amax[PASSES];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) unpack8(qw[ps], x[ps]);
+    row_amax<D, GRAN, PASSES>(x, amax, &blk_amax[0]);
+    store_rows<D, QK, GRAN, PASSES>(x, amax, tok0, rr, c8, fold, qc + co, qs + sco, tid);
+  }
+
+  // ---- V -------------------------------------------------------------------------
+  if (PV == kPV_FP8) {
+    float x[4][8], cm[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) unpack8(vw[i], x[i]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cm[e] = fmaxf(fmaxf(fabsf(x[0][e]), fabsf(x[1][e])), fmaxf(fabsf(x[2][e]), fabsf(x[3][e])));
+    // across the token groups of this wave (lanes c8 + LPR*m), then across waves
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (LPR == 8) {
+        cm[e] = fmaxf(cm[e], __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(cm[e]), 0x128, 0xf, 0xf, false)));  // row_ror:8
+      }
+      cm[e] = rows_max(cm[e]);
+    }
+    if (tid < VTHREADS && (tid & 63) < LPR) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vmax[wave][c8 * 8 + e] = cm[e];
+    }
+    __syncthreads();
+    constexpr int VW = VTHREADS / 64;  // waves holding V
+    if (tid < VTHREADS) {
+      float am[8];
+      {
+        const f32x4* v4 = reinterpret_cast<const f32x4*>(&vmax[0][c8 * 8]);
+        const f32x4 a0 = v4[0], a1 = v4[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          am[i] = a0[i];
+          am[4 + i] = a1[i];
+        }
+#pragma unroll
+        for (int ww = 1; ww < VW; ++ww) {
+          const f32x4* w4 = reinterpret_cast<const f32x4*>(&vmax[ww][c8 * 8]);
+          const f32x4 b0 = w4[0], b1 = w4[1];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            am[i] = fmaxf(am[i], b0[i]);
+            am[4 + i] = fmaxf(am[4 + i], b1[i]);
+          }
+        }
+      }
+      float inv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) inv[e] = kFp8Max / fmaxf(am[e], kEps);
+      if (g == 0) {
+        f32x4* o4 = reinterpret_cast<f32x4*>(vs + ((int64_t)bh * (np / 64) + blk) * D + c8 * 8);
+        o4[0] = f32x4{am[0] / kFp8Max, am[1] / kFp8Max, am[2] / kFp8Max, am[3] / kFp8Max};
+        o4[1] = f32x4{am[4] / kFp8Max, am[5] / kFp8Max, am[6] / kFp8Max, am[7] / kFp8Max};
+      }
+      // word of channel d = 32j + r for tokens 4g..4g+3 -> chunk (j, b, L = 32h + r), byte 4jj,
+      // with g = 8b + 2jj + h
+      const int b = g >> 3, jj = (g >> 1) & 3, hh = g & 1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = c8 * 8 + e, j = d >> 5, r = d & 31;
+        const uint32_t word = pack_fp8x4(x[0][e] * inv[e], x[1][e] * inv[e], x[2][e] * inv[e], x[3][e] * inv[e]);
+        *reinterpret_cast<uint32_t*>(vimg + (((j * 2 + b) * 64 + 32 * hh + r) * 16) + 4 * jj) = word;
+      }
+    }
+  } else if (tid < VTHREADS) {
+    // bf16 V: element 4jj + i of chunk (j, b, tt, L) = V[32b + 16tt + 8jj + 4h + i][32j + r],
+    // with g = 8b + 4tt + 2jj + h
+    const int b = g >> 3, tt = (g >> 2) & 1, jj = (g >> 1) & 1, hh = g & 1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = c8 * 8 + e, j = d >> 5, r = d & 31;
+      const int sh = (e & 1) * 16;
+      uint32_t t4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t4[i] = (word_of(vw[i], e >> 1) >> sh) & 0xffffu;
+      uint2 pk;
+      pk.x = t4[0] | (t4[1] << 16);
+      pk.y = t4[2] | (t4[3] << 16);
+      *reinterpret_cast<uint2*>(vimg + (((((j * 2 + b) * 2 + tt) * 64 + 32 * hh + r) * 8) + 4 * jj) * 2) = pk;
+    }
+  }
+  __syncthreads();
+  {
+    constexpr int VBYTES = (PV == kPV_FP8 ? 1 : 2) * 64 * D;
+    uint8_t* vo = vout + (PV == kPV_FP8 ? 1 : 2) * (co + tok0 * D);
+#pragma unroll
+    for (int i = tid; i < VBYTES / 16; i += 256)
+      reinterpret_cast<uint4*>(vo)[i] = reinterpret_cast<const uint4*>(vimg)[i];
+  }
+
+  // ---- K: codes right away without smoothing; with smoothing, this block's
+  // fp64 column sums (exact) for the mean, and k_quantize_kernel does the codes
+  if constexpr (!SMOOTH) {
+    float x[PASSES][8], amax[PASSES];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) unpack8(kw[ps], x[ps]);
+    row_amax<D, GRAN, PASSES>(x, amax, &blk_amax[1]);
+    store_rows<D, QK, GRAN, PASSES>(x, amax, tok0, rr, c8, 1.0f, kc + co, ks + sco, tid);
+  } else {
+    double cs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cs[e] = 0.0;
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      float x[8];
+      unpack8(kw[ps], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cs[e] += (double)x[e];
+    }
+    // token rows of the wave (lanes c8 + LPR*m), then the 4 waves
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) cs[e] += __shfl_xor(cs[e], off);
+    if ((tid & 63) < LPR) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ksw[wave][c8 * 8 + e] = cs[e];
+    }
+    __syncthreads();
+    // fp64 sums of bf16 values are exact, so the order of these additions
+    // does not change the result
+    if (tid < D) unsafeAtomicAdd(&ksum[(int64_t)bh * D + tid], (ksw[0][tid] + ksw[1][tid]) + (ksw[2][tid] + ksw[3][tid]));
+  }
+}
+
+// Zero the per-head K column sums before quantize accumulates into them.
+__global__ void __launch_bounds__(256) k_sum_zero_kernel(double* __restrict__ ksum, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) ksum[i] = 0.0;
+}
+
+// Pass 2 (smoothing on): K codes, one workgroup per (64-token block, bh).
+// The head's mean is its column sum / N in fp64, rounded to fp32 then bf16
+// (the reference's bf16 mean); K rows are smoothed as bf16(k - mean).
+template <int D, int QK, int GRAN>
+__global__ void __launch_bounds__(256) k_quantize_kernel(const uint16_t* __restrict__ k, int64_t n, int64_t np,
+                                                         const double* __restrict__ ksum, uint8_t* __restrict__ kc,
+                                                         float* __restrict__ ks, uint16_t* __restrict__ kmean) {
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   constexpr int PASSES = 64 / RPP;
   __shared__ float mu[D];
-  __shared__ unsigned int amax_u[2 + D];
-  __shared__ __attribute__((aligned(16))) uint8_t vt[(PV == kPV_FP8 ? 1 : 2) * 64 * D];
+  __shared__ unsigned int blk_amax;
   const int bh = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+  const int c8 = tid % LPR, rr = tid / LPR;
   const int64_t tok0 = (int64_t)blk * 64;
-  if (tid < 2 + D) amax_u[tid] = 0u;
-  if (SMOOTH && tid < D) {
-    double s = 0.0;
-    for (int c = 0; c < nchunks; ++c) s += ws[((int64_t)bh * nchunks + c) * D + tid];
-    const uint16_t m16 = f32_to_bf16_rne((float)(s / (double)n));
+  const int64_t so = (int64_t)bh * n * D;
+  const int64_t co = (int64_t)bh * np * D;
+  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+  uint4 w[PASSES];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int64_t tok = min(tok0 + rr + ps * RPP, n - 1);  // clamped, masked below
+    w[ps] = *reinterpret_cast<const uint4*>(k + so + tok * D + c8 * 8);
+  }
+  if (tid == 0) blk_amax = 0u;
+  if (tid < D) {
+    const uint16_t m16 = f32_to_bf16_rne((float)(ksum[(int64_t)bh * D + tid] / (double)n));
     mu[tid] = bf16_to_f32(m16);
     if (blk == 0) kmean[(int64_t)bh * D + tid] = m16;
   }
   __syncthreads();
-  const int64_t so = (int64_t)bh * n * D;
-  const int64_t co = (int64_t)bh * np * D;
-  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
-  quantize_rows<D, QK, GRAN, false>(q + so, n, np, tok0, mu, fold, qc + co, qs + sco, &amax_u[0]);
-  quantize_rows<D, QK, GRAN, SMOOTH>(k + so, n, np, tok0, mu, 1.0f, kc + co, ks + sco, &amax_u[1]);
-
-  // V: stage this 64-token tile in LDS, then write the transposed fragments.
-  const int c8 = tid % LPR, rr = tid / LPR;
-  if (PV == kPV_FP8) {
-    float x[PASSES][8];
-    float cm[8];
+  float x[PASSES][8], amax[PASSES];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) cm[e] = 0.0f;
+  for (int ps = 0; ps < PASSES; ++ps) {
+    unpack8(w[ps], x[ps]);
+    const float keep = tok0 + rr + ps * RPP < n ? 1.0f : 0.0f;
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      load8<D>(v + so, tok0 + rr + ps * RPP, n, c8, x[ps]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) cm[e] = fmaxf(cm[e], fabsf(x[ps][e]));
-    }
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) cm[e] = fmaxf(cm[e], __shfl_xor(cm[e], off));
-    if ((tid & 63) < LPR) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) atomicMax(&amax_u[2 + c8 * 8 + e], __float_as_uint(cm[e]));
-    }
-    __syncthreads();
-    float inv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) inv[e] = kFp8Max / fmaxf(__uint_as_float(amax_u[2 + c8 * 8 + e]), kEps);
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      const int row = rr + ps * RPP;
-      uint2 word;
-      word.x = pack_fp8x4(x[ps][0] * inv[0], x[ps][1] * inv[1], x[ps][2] * inv[2], x[ps][3] * inv[3]);
-      word.y = pack_fp8x4(x[ps][4] * inv[4], x[ps][5] * inv[5], x[ps][6] * inv[6], x[ps][7] * inv[7]);
-      *reinterpret_cast<uint2*>(vt + row * D + c8 * 8) = word;
-    }
-    if (tid < D) vs[((int64_t)bh * (np / 64) + blk) * D + tid] = __uint_as_float(amax_u[2 + tid]) / kFp8Max;
-    __syncthreads();
-    // 16-byte chunk (j, b, L): byte 4*jj + i = Vc[32b + 8jj + 4h + i][32j + r]
-    constexpr int CHUNKS = (D / 32) * 2 * 64;
-    uint8_t* vo = vout + co + tok0 * D;
-    for (int ch = tid; ch < CHUNKS; ch += 256) {
-      const int L = ch & 63, b = (ch >> 6) & 1, j = ch >> 7;
-      const int h = L >> 5, r = L & 31, d = 32 * j + r;
-      uint32_t w4[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int key = 32 * b + 8 * jj + 4 * h;
-        w4[jj] = (uint32_t)vt[(key + 0) * D + d] | ((uint32_t)vt[(key + 1) * D + d] << 8) |
-                 ((uint32_t)vt[(key + 2) * D + d] << 16) | ((uint32_t)vt[(key + 3) * D + d] << 24);
-      }
-      *reinterpret_cast<uint4*>(vo + (int64_t)ch * 16) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-    }
-  } else {
-    uint16_t* vt16 = reinterpret_cast<uint16_t*>(vt);
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      const int row = rr + ps * RPP;
-      const int64_t tok = tok0 + row;
-      uint4 w = make_uint4(0, 0, 0, 0);
-      if (tok < n) w = *reinterpret_cast<const uint4*>(v + so + tok * D + c8 * 8);
-      *reinterpret_cast<uint4*>(vt16 + row * D + c8 * 8) = w;
-    }
-    __syncthreads();
-    // 16-byte chunk (j, b, tt, L): element 4*jj + i = V[32b + 16tt + 8jj + 4h + i][32j + r]
-    constexpr int CHUNKS = (D / 32) * 4 * 64;
-    uint8_t* vo = vout + 2 * (co + tok0 * D);
-    for (int ch = tid; ch < CHUNKS; ch += 256) {
-      const int L = ch & 63, tt = (ch >> 6) & 1, b = (ch >> 7) & 1, j = ch >> 8;
-      const int h = L >> 5, r = L & 31, d = 32 * j + r;
-      uint32_t w4[4];
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int key = 32 * b + 16 * tt + 8 * jj + 4 * h;
-        w4[2 * jj] = (uint32_t)vt16[(key + 0) * D + d] | ((uint32_t)vt16[(key + 1) * D + d] << 16);
-        w4[2 * jj + 1] = (uint32_t)vt16[(key + 2) * D + d] | ((uint32_t)vt16[(key + 3) * D + d] << 16);
-      }
-      *reinterpret_cast<uint4*>(vo + (int64_t)ch * 16) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-    }
+    for (int e = 0; e < 8; ++e) x[ps][e] = bf16_to_f32(f32_to_bf16_rne(x[ps][e] - mu[c8 * 8 + e])) * keep;
   }
+  row_amax<D, GRAN, PASSES>(x, amax, &blk_amax);
+  store_rows<D, QK, GRAN, PASSES>(x, amax, tok0, rr, c8, 1.0f, kc + co, ks + sco, tid);
 }
 
 template <int D, int QK, int PV, int GRAN, bool SMOOTH>
@@ -250,12 +353,16 @@ hipError_t launch_quantize_t(const uint16_t* q, const uint16_t* k, const uint16_
                              float fold, double* ws, uint8_t* qc, float* qs, uint8_t* kc, float* ks,
                              uint8_t* vout, float* vs, uint16_t* kmean, hipStream_t st) {
   const int64_t np = padded_len(n);
-  const int nchunks = (int)((n + kSumChunk - 1) / kSumChunk);
+  const int nblk = (int)(np / 64);
   if (SMOOTH) {
-    hipLaunchKernelGGL((k_colsum_kernel<D>), dim3(nchunks, (unsigned)bh), dim3(256), 0, st, k, n, ws, nchunks);
+    hipLaunchKernelGGL(k_sum_zero_kernel, dim3((unsigned)((bh * D + 255) / 256)), dim3(256), 0, st, ws, bh * D);
   }
-  hipLaunchKernelGGL((quantize_kernel<D, QK, PV, GRAN, SMOOTH>), dim3((unsigned)(np / 64), (unsigned)bh),
-                     dim3(256), 0, st, q, k, v, n, np, fold, ws, nchunks, qc, qs, kc, ks, vout, vs, kmean);
+  hipLaunchKernelGGL((quantize_kernel<D, QK, PV, GRAN, SMOOTH>), dim3((unsigned)nblk, (unsigned)bh), dim3(256), 0,
+                     st, q, k, v, n, np, fold, ws, qc, qs, kc, ks, vout, vs);
+  if (SMOOTH) {
+    hipLaunchKernelGGL((k_quantize_kernel<D, QK, GRAN>), dim3((unsigned)nblk, (unsigned)bh), dim3(256), 0, st, k, n,
+                       np, ws, kc, ks, kmean);
+  }
   return hipGetLastError();
 }
 
@@ -297,9 +404,10 @@ hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t
   return hipErrorInvalidValue;
 }
 
+// fp64 column sums of K per head, [bh][d].
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d) {
-  const int64_t nchunks = (n + kSumChunk - 1) / kSumChunk;
-  return (size_t)(bh * nchunks * d) * sizeof(double);
+  (void)n;
+  return (size_t)(bh * d) * sizeof(double);
 }
 
 }  // namespace sage

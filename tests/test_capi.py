@@ -43,7 +43,7 @@ def test_sizes_and_padding():
     from futudiffu_amd import _lib
     lib = _lib.load()
     assert [lib.sage_padded_len(n) for n in (1, 128, 129, 4416)] == [128, 128, 256, 4480]
-    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 18 * 128 * 8
+    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 128 * 8
     assert lib.sage_attn_workspace_bytes(2, 200) == 2 * (4 + 256 // 32 + 256 // 128) * 16
 
 
