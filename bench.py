@@ -64,6 +64,35 @@ def quant_bytes(B, H, N, D, pv, gran):
     return rd + wr
 
 
+def profiled_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs of this same workload (scaled by the copy calibration), or
+    None when no profile of this workload is committed."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "sage_fwd_int8qk_fp8pv_B1H30N4416D128_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except OSError:
+        return None
+    if not workload.startswith(t["workload"]) or kernel not in t["kernels"]:
+        return None
+    k = t["kernels"][kernel]
+    sc = t["counter_scale"]
+    return round((k["fetch_kib"] * sc["FETCH_SIZE"] + k["write_kib"] * sc["WRITE_SIZE"]) * 1024)
+
+
+def attn_bytes(B, H, N, D, pv, gran):
+    """Algorithmic HBM bytes of one attention launch: codes, scales and V read once,
+    output and LSE written once."""
+    bh = B * H
+    nsc = N if gran == "token" else (N + 63) // 64
+    rd = 2 * bh * N * D + 2 * bh * nsc * 4 + bh * N * D * (1 if pv == "fp8" else 2)
+    if pv == "fp8":
+        rd += bh * ((N + 63) // 64) * D * 4
+    return rd + bh * N * D * 2 + bh * N * 4
+
+
 def cpu_baseline(args, flop_per_head):
     """Time the CPU oracle on whole heads of the same workload (bounded sample)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
@@ -172,6 +201,8 @@ def main():
     q_avg = sum(qms) / len(qms)
     a_avg = sum(ams) / len(ams)
 
+    workload = (f"sage_attn_fwd B={B} H={H} N={N} D={D} {args.qk}-QK {args.pv}-PV "
+                f"{args.granularity} scales, no mask (quantize + fused attention)")
     attn_tflops = flop / (a_avg * 1e-3) / 1e12
     peak = PEAK_8BIT_TFLOPS
     qbytes = quant_bytes(B, H, N, D, args.pv, args.granularity)
@@ -191,8 +222,7 @@ def main():
         "dtype": f"{args.qk}-qk/{args.pv}-pv",
         "data": "synthetic: q,k,v ~ N(0,1) bf16, K += N(0,2) per channel, seed 0",
         "config": {
-            "workload": (f"sage_attn_fwd B={B} H={H} N={N} D={D} {args.qk}-QK {args.pv}-PV "
-                         f"{args.granularity} scales, no mask (quantize + fused attention)"),
+            "workload": workload,
             "B": B, "H": H, "N": N, "D": D, "qk": args.qk, "pv": args.pv,
             "granularity": args.granularity, "parallelism": "single GPU",
         },
@@ -204,14 +234,16 @@ def main():
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / peak, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(workload, "attn_fwd_kernel"),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0)",
+            "algorithmic_bytes": attn_bytes(B, H, N, D, args.pv, args.granularity),
             "avg_kernel_ms": round(a_avg, 5),
             "median_kernel_ms": round(ams[len(ams) // 2], 5),
             "flop_per_launch": flop,
         },
         "quantize": {
             "bound": "hbm",
-            "kernel": "k_colsum_kernel + quantize_kernel",
+            "kernel": "k_sum_zero_kernel + quantize_kernel + k_quantize_kernel",
             "achieved": round(q_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

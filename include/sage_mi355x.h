@@ -81,7 +81,8 @@ const char* sage_last_error(void);
 /* Np for a sequence length: N rounded up to a multiple of 128. */
 int64_t sage_padded_len(int64_t n);
 
-/* Bytes of device workspace sage_quantize_qkv needs (fp64 partial K sums). */
+/* Bytes of device workspace sage_quantize_qkv needs when smoothing: the
+ * per-head fp64 column sums of K, [bh][d] (cleared and filled by the call). */
 size_t sage_quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
 
 /* K smoothing + Q/K (and, for fp8 PV, V) quantization.
@@ -105,7 +106,9 @@ int sage_quantize_qkv(const void* q, const void* k, const void* v,
                       void* workspace, size_t workspace_bytes,
                       hipStream_t stream);
 
-/* Bytes of device workspace sage_attn_fwd needs when doc_ids is given. */
+/* Bytes of device workspace sage_attn_fwd needs when doc_ids is given:
+ * per-batch (min doc, max doc, #valid, #padding) summaries of every 64-key
+ * tile and every 32- and 128-row query block. */
 size_t sage_attn_workspace_bytes(int64_t b, int64_t n);
 
 /* Fused attention forward over pre-quantized operands.
