@@ -35,6 +35,8 @@
 // dequantized by 2^(bm - m_ref) / 448 per row and the V scale per channel.
 // bf16 P is 2^(s - m_ref) rounded to bf16; bf16 rounding is relative, so this
 // matches the reference's bf16(2^(s - m)) up to exp2 rounding.
+#include <algorithm>
+
 #include "sage_common.h"
 #include "sage_launch.h"
 
@@ -187,8 +189,14 @@ __device__ __forceinline__ void qk_half(const uint8_t* sb, const i32x4* qf, int 
 // Per-row values for the O fragment: lane (h, r) holds rows 8j + 4h + i,
 // element 4j + i.  Lanes h = 0 publish their row's value in the wave's
 // 32-float exchange; every lane then reads four broadcast float4s.
+// The exchange passes values between lanes, which a single-lane view of the
+// program does not see: wavefront-scope fences around it keep the compiler
+// from reusing an earlier call's reads in a later call.
 __device__ __forceinline__ void rows_of(float* xrow, float v, int h, int r, float out[16]) {
   if (h == 0) xrow[r] = v;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const f32x4* x4 = reinterpret_cast<const f32x4*>(xrow);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -340,22 +348,29 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
   }
 }
 
+// Tiles [t_begin, t_end) of work item (bh, query tile qt) for this wave:
+// leaves the wave's O, reference point and row-sum half in o / m_ref / l_acc
+// (O and l in the frame of m_ref; all zero / -inf for a wave past N).
+// Ends with a workgroup barrier, after which the stage ring may be reused.
 template <int D, int QK, int PV, int GRAN, int MASK>
-__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
+__device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, int bh, int qt, int t_begin,
+                                           int t_end, f32x16* o, float& m_ref, float& l_acc) {
   using St = Stage<D, PV>;
   using SM = Smem<D, PV>;
   using SAcc = typename SAccT<QK>::type;
   constexpr int NC = D / 32;  // 32-channel chunks
-  __shared__ __attribute__((aligned(16))) uint8_t smem[SM::bytes];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int h = lane >> 5, r = lane & 31;
+  const int r = lane & 31;
   const int nq = (int)(p.np / kRowsPerWG);
-  int bh, qt;
-  item_of(blockIdx.x, (int)gridDim.x, p.bh, nq, p.light_last, bh, qt);
   const int bidx = bh / p.h;
   const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * wave;  // first query row of this wave
   const bool wave_live = q0 < p.n;
   float* xrow = reinterpret_cast<float*>(smem + SM::offX) + 32 * wave;
+
+  m_ref = -INFINITY;
+  l_acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) o[j] = f32x16{0};
 
   // ---- per-wave query state ------------------------------------------------
   i32x4 qf[NC];
@@ -380,20 +395,13 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
     qsum128 = p.q_sum128[(int64_t)bidx * nq + qt];
   }
 
-  // Row state in a lazily moved frame: O and l hold sums of 2^(s - m_ref).
-  float m_ref = -INFINITY;
-  float l_acc = 0.0f;
-  f32x16 o[NC];
-#pragma unroll
-  for (int j = 0; j < NC; ++j) o[j] = f32x16{0};
-
   const uint8_t* kg = p.kc + (int64_t)bh * p.np * D;
   const uint8_t* vg = p.vin + (int64_t)bh * p.np * D * (PV == kPV_FP8 ? 1 : 2);
   const int32_t* docb = (MASK & 2) ? p.doc + (int64_t)bidx * p.n : nullptr;
 
   // ---- tile schedule: active tiles in order ----------------------------------
   auto next_active = [&](int t) -> int {
-    for (; t < p.nt; ++t) {
+    for (; t < t_end; ++t) {
       if (MASK & 1) {
         if (p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] == 0) continue;
       }
@@ -467,32 +475,32 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   } while (0)
 
   // ---- prologue: tiles 0 and 1 of the schedule in stages 0 and 1 --------------
-  int t = next_active(0);
-  int t1 = t < p.nt ? next_active(t + 1) : p.nt;
-  int t2 = t1 < p.nt ? next_active(t1 + 1) : p.nt;
-  if (t < p.nt) {
+  int t = next_active(t_begin);
+  int t1 = t < t_end ? next_active(t + 1) : t_end;
+  int t2 = t1 < t_end ? next_active(t1 + 1) : t_end;
+  if (t < t_end) {
     SAGE_LOAD_TILE(t);
     SAGE_STORE_TILE(0);
   }
-  if (t1 < p.nt) {
+  if (t1 < t_end) {
     SAGE_LOAD_TILE(t1);
     SAGE_STORE_TILE(1);
   }
   __syncthreads();
   SAcc s0, s1;  // S^T of the tile about to be consumed
-  if (t < p.nt && wave_live) {
+  if (t < t_end && wave_live) {
     qk_half<D, QK>(smem, qf, lane, 0, s0);
     qk_half<D, QK>(smem, qf, lane, 1, s1);
   }
 
   int stage = 0;
-  while (t < p.nt) {
-    if (t2 < p.nt) SAGE_LOAD_TILE(t2);
+  while (t < t_end) {
+    if (t2 < t_end) SAGE_LOAD_TILE(t2);
     const uint8_t* sb = smem + stage * St::bytes;
     const int stage1 = stage == 2 ? 0 : stage + 1;
     const int stage2 = stage1 == 2 ? 0 : stage1 + 1;
     // the last tile recomputes its own S^T in place of a next tile's (unused)
-    const uint8_t* sb_next = t1 < p.nt ? smem + stage1 * St::bytes : sb;
+    const uint8_t* sb_next = t1 < t_end ? smem + stage1 * St::bytes : sb;
 
     int cls = wave_live ? 1 : 0;
     if ((MASK & 2) && cls) cls = classify(qsum, p.kv_sum[(int64_t)bidx * p.nt + t]);
@@ -500,26 +508,41 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
       tile_body<D, QK, PV, GRAN, MASK, true>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq);
     else if (cls == 1)
       tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq);
-    else if (wave_live && t1 < p.nt) {
+    else if (wave_live && t1 < t_end) {
       qk_half<D, QK>(sb_next, qf, lane, 0, s0);
       qk_half<D, QK>(sb_next, qf, lane, 1, s1);
     }
 
     // ---- hand over: tile t2 into the stage tile t - 1 used ----------------------
-    if (t2 < p.nt) SAGE_STORE_TILE(stage2);
+    if (t2 < t_end) SAGE_STORE_TILE(stage2);
     __syncthreads();
     stage = stage1;
     t = t1;
     t1 = t2;
-    t2 = t2 < p.nt ? next_active(t2 + 1) : p.nt;
+    t2 = t2 < t_end ? next_active(t2 + 1) : t_end;
   }
 #undef SAGE_LOAD_TILE
 #undef SAGE_STORE_TILE
 #undef SAGE_CHUNK_LD
 #undef SAGE_CHUNK_ST
+}
 
-  // ---- epilogue: LSE, normalize, stage bf16 rows in LDS, 16-byte stores --------
-  if (!wave_live) return;  // no barrier follows
+constexpr int kRawBufferWord3 = 0x00020000;  // word 3 of a raw (untyped) buffer resource, gfx9 family
+
+// Normalize and store this wave's 32 rows of item (bh, qt) and their LSE.
+// Stages bf16 rows in the stage ring (free after item_tiles' final barrier)
+// for 16-byte stores.
+template <int D, int PV>
+__device__ __forceinline__ void store_rows_final(const AttnParams& p, uint8_t* smem, int bh, int qt, f32x16* o,
+                                                 float m_ref, float l_acc) {
+  using SM = Smem<D, PV>;
+  constexpr int NC = D / 32;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
+  const int h = lane >> 5, r = lane & 31;
+  const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * wave;
+  if (q0 >= p.n) return;  // wave past N: nothing to store (no barrier inside)
+  float* xrow = reinterpret_cast<float*>(smem + SM::offX) + 32 * wave;
   float l_tot;
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_acc), __float_as_uint(l_acc), false, false);
@@ -538,16 +561,32 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
   __builtin_amdgcn_wave_barrier();
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  uint16_t* ob = p.out + ((int64_t)bh * p.n + q0) * D;
+  // 16-byte stores through a buffer resource that ends at row N: the hardware
+  // drops the stores of rows past N
+  const int rows = p.n - q0 < 32 ? (int)(p.n - q0) : 32;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(p.out + ((int64_t)bh * p.n + q0) * D, 0, rows * D * 2, kRawBufferWord3);
 #pragma unroll
-  for (int i = 0; i < 32 * CPR / 64; ++i) {
-    const int ch = lane + 64 * i;
-    const int row = ch / CPR, col = ch % CPR;
-    if (q0 + row < p.n)
-      *reinterpret_cast<uint4*>(ob + (int64_t)row * D + col * 8) =
-          *reinterpret_cast<const uint4*>(ep + row * D + col * 8);
+  for (int i = 0; i < 32 * D * 2 / (16 * 64); ++i) {
+    const int off = (lane + 64 * i) * 16;  // row-major bytes: row off / (2D), column (off % 2D) / 2
+    const i32x4 v = *reinterpret_cast<const i32x4*>(reinterpret_cast<const uint8_t*>(ep) + off);
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
   }
+}
+
+template <int D, int QK, int PV, int GRAN, int MASK>
+__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
+  using SM = Smem<D, PV>;
+  constexpr int NC = D / 32;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SM::bytes];
+  f32x16 o[NC];
+  float m_ref, l_acc;
+  const int nq = (int)(p.np / kRowsPerWG);
+
+  int bh, qt;
+  item_of(blockIdx.x, (int)gridDim.x, p.bh, nq, p.light_last, bh, qt);
+  item_tiles<D, QK, PV, GRAN, MASK>(p, smem, bh, qt, 0, p.nt, o, m_ref, l_acc);
+  store_rows_final<D, PV>(p, smem, bh, qt, o, m_ref, l_acc);
 }
 
 // int32 QK^T of int8 codes through the attention kernel's MFMA fragments.
@@ -627,10 +666,17 @@ hipError_t launch_qk_int32(const uint8_t* qc, const uint8_t* kc, int64_t bh, int
   return hipGetLastError();
 }
 
-size_t attn_workspace_bytes(int64_t b, int64_t n) {
+AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d) {
+  (void)h;
+  (void)d;
   const int64_t np = padded_len(n);
   const int64_t nt = (n + 63) / 64;
-  return (size_t)(b * (nt + np / 32 + np / 128)) * sizeof(int4);
+  AttnWorkspace w;
+  w.doc_off = 0;
+  w.bytes = (size_t)(b * (nt + np / 32 + np / 128)) * sizeof(int4);
+  return w;
 }
+
+size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) { return attn_workspace(b, h, n, d).bytes; }
 
 }  // namespace sage

@@ -52,7 +52,9 @@ int64_t sage_padded_len(int64_t n) { return sage::padded_len(n); }
 
 size_t sage_quant_workspace_bytes(int64_t bh, int64_t n, int64_t d) { return sage::quant_workspace_bytes(bh, n, d); }
 
-size_t sage_attn_workspace_bytes(int64_t b, int64_t n) { return sage::attn_workspace_bytes(b, n); }
+size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) {
+  return sage::attn_workspace_bytes(b, h, n, d);
+}
 
 int sage_quantize_qkv(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t d, int qk_kind,
                       int pv_kind, int granularity, int smooth_k, float sm_scale_log2e, void* q_codes,
@@ -108,14 +110,15 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
   }
   sage::AttnParams p;
   memset(&p, 0, sizeof(p));
+  const sage::AttnWorkspace ws = sage::attn_workspace(b, h, n, d);
+  if (!workspace || workspace_bytes < ws.bytes)
+    return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", ws.bytes, workspace_bytes);
+  if (!aligned16(workspace)) return fail(SAGE_ERR_ALIGN, "workspace must be 16-byte aligned");
+  uint8_t* wsp = static_cast<uint8_t*>(workspace);
   if (doc_ids) {
-    const size_t need = sage::attn_workspace_bytes(b, n);
-    if (!workspace || workspace_bytes < need)
-      return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need, workspace_bytes);
-    if (!aligned16(workspace)) return fail(SAGE_ERR_ALIGN, "workspace must be 16-byte aligned");
     mask |= 2;
     const int64_t nt = nkv;
-    p.kv_sum = static_cast<const int4*>(workspace);
+    p.kv_sum = reinterpret_cast<const int4*>(wsp + ws.doc_off);
     p.q_sum = p.kv_sum + b * nt;
     p.q_sum128 = p.q_sum + b * (sage::padded_len(n) / 32);
   }

@@ -37,7 +37,12 @@ hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
 
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb, hipStream_t st);
-size_t attn_workspace_bytes(int64_t b, int64_t n);
+// Workspace of one attention call: the doc-id summaries.
+struct AttnWorkspace {
+  size_t doc_off, bytes;
+};
+AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d);
+size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
 hipError_t launch_qk_int32(const uint8_t* qc, const uint8_t* kc, int64_t bh, int64_t n, int64_t d, int32_t* s,
                            hipStream_t st);
 

@@ -165,14 +165,12 @@ def attn_from_quantized(qz: SageQuantized, B: int, H: int, *, block_mask: Tensor
     BH, N, D = B * H, qz.n, qz.d
     dev = qz.q_codes.device
     bm, stride_z, nq, nkv = _norm_mask(block_mask, BH, N, dev)
-    ws = None
-    wsb = 0
     if doc_ids is not None:
         if doc_ids.shape != (B, N):
             raise ValueError(f"doc_ids must be [B, N] = [{B}, {N}], got {tuple(doc_ids.shape)}")
         doc_ids = doc_ids.to(device=dev, dtype=torch.int32).contiguous()
-        wsb = int(lib.sage_attn_workspace_bytes(B, N))
-        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    wsb = int(lib.sage_attn_workspace_bytes(B, H, N, D))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     if out is None:
         out = torch.empty(B, H, N, D, dtype=torch.bfloat16, device=dev)
     if lse is None:

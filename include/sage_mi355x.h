@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 1
+#define SAGE_ABI_VERSION 2
 
 enum sage_status {
   SAGE_OK = 0,
@@ -106,10 +106,12 @@ int sage_quantize_qkv(const void* q, const void* k, const void* v,
                       void* workspace, size_t workspace_bytes,
                       hipStream_t stream);
 
-/* Bytes of device workspace sage_attn_fwd needs when doc_ids is given:
- * per-batch (min doc, max doc, #valid, #padding) summaries of every 64-key
- * tile and every 32- and 128-row query block. */
-size_t sage_attn_workspace_bytes(int64_t b, int64_t n);
+/* Bytes of device workspace sage_attn_fwd needs for B x H heads of N tokens
+ * of dimension D: per-batch (min doc, max doc, #valid, #padding) summaries of
+ * every 64-key tile and 32- and 128-row query block (written and used when
+ * doc_ids is given).  No reference counterpart (the Triton launch needs no
+ * workspace). */
+size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
 
 /* Fused attention forward over pre-quantized operands.
  * Replaces the launch of _sage_attn_fwd_int8qk_bf16pv_masked_lse
@@ -123,8 +125,11 @@ size_t sage_attn_workspace_bytes(int64_t b, int64_t n);
  *   doc_ids       optional int32 [B, N] per-token document ids for exact
  *                 masking: key n is visible to query m iff doc[n] >= 0 and
  *                 (doc[m] == doc[n] or doc[m] < 0).  Fully masked tiles issue
- *                 no MFMA.  Needs workspace of sage_attn_workspace_bytes.
- *   h             heads per batch (row z of q belongs to batch z / h). */
+ *                 no MFMA.
+ *   h             heads per batch (row z of q belongs to batch z / h).
+ *   workspace     device memory of sage_attn_workspace_bytes(b, h, n, d)
+ *                 bytes, 16-byte aligned.  Concurrent calls need separate
+ *                 workspaces. */
 int sage_attn_fwd(const void* q_codes, const float* q_scale,
                   const void* k_codes, const float* k_scale,
                   const void* v_in, const float* v_scale,

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), f"{name} declared in the header but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes prototype"
-    assert lib.sage_abi_version() == 1
+    assert lib.sage_abi_version() == 2
 
 
 def test_sizes_and_padding():
@@ -44,7 +44,10 @@ def test_sizes_and_padding():
     lib = _lib.load()
     assert [lib.sage_padded_len(n) for n in (1, 128, 129, 4416)] == [128, 128, 256, 4480]
     assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 128 * 8
-    assert lib.sage_attn_workspace_bytes(2, 200) == 2 * (4 + 256 // 32 + 256 // 128) * 16
+    # per-batch summaries of every 64-key tile and 32- and 128-row query block
+    for b, h, n, d in ((2, 3, 200, 128), (1, 30, 4416, 128), (1, 1, 1, 64)):
+        np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
+        assert lib.sage_attn_workspace_bytes(b, h, n, d) == b * (nt + np_ // 32 + np_ // 128) * 16
 
 
 def _quant_call(lib, **over):
@@ -90,7 +93,9 @@ def _attn_call(lib, **over):
     (dict(d=64 + 32), 1, "head_dim"),
     (dict(mask=256, nq=2), 1, "block_mask must be 3 x 5"),
     (dict(mask=256, sz=7), 1, "mask_stride_z"),
+    (dict(ws=None), 3, "workspace"),
     (dict(doc=256, ws=None), 3, "workspace"),
+    (dict(ws=256, wsb=100), 3, "workspace of"),
     (dict(doc=256, ws=264, wsb=1 << 20), 2, "workspace must be 16-byte aligned"),
     (dict(out=None), 1, "null"),
     (dict(pv=1, vs=None), 1, "v_scale"),
