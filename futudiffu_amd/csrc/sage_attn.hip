@@ -253,12 +253,20 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
   }
 
   // ---- row max: max3 tree, then across the two lane halves --------------------
-  float m4[4];
+  float mx;
+  {
+    // 32 values -> 10 + 2 -> 4 -> 2 -> 1 with three-input maxima (v_max3_f32)
+    auto max3 = [](float a, float b, float c) { return __builtin_fmaxf(__builtin_fmaxf(a, b), c); };
+    const float* w = &u[0][0];
+    float l1[12];
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
-    m4[k] = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(u[0][4 * k], u[0][4 * k + 1]), __builtin_fmaxf(u[0][4 * k + 2], u[0][4 * k + 3])),
-                            __builtin_fmaxf(__builtin_fmaxf(u[1][4 * k], u[1][4 * k + 1]), __builtin_fmaxf(u[1][4 * k + 2], u[1][4 * k + 3])));
-  float mx = __builtin_fmaxf(__builtin_fmaxf(m4[0], m4[1]), __builtin_fmaxf(m4[2], m4[3]));
+    for (int k = 0; k < 10; ++k) l1[k] = max3(w[3 * k], w[3 * k + 1], w[3 * k + 2]);
+    l1[10] = w[30];
+    l1[11] = w[31];
+    const float l2a = max3(l1[0], l1[1], l1[2]), l2b = max3(l1[3], l1[4], l1[5]);
+    const float l2c = max3(l1[6], l1[7], l1[8]), l2d = max3(l1[9], l1[10], l1[11]);
+    mx = __builtin_fmaxf(max3(l2a, l2b, l2c), l2d);
+  }
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
     mx = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
@@ -574,6 +582,25 @@ __device__ __forceinline__ void store_rows_final(const AttnParams& p, uint8_t* s
   }
 }
 
+// Partial result of a piece of a split item: O in lane order (element e of
+// chunk c of wave w at ((w*NC + c)*16 + e)*64 + lane), then m_ref and l_acc
+// per lane.  Buffer stores: the per-element offsets are scalar constants.
+template <int D>
+__device__ __forceinline__ void store_partial(float* slot, const f32x16* o, float m_ref, float l_acc) {
+  constexpr int NC = D / 32;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(slot, 0, (int)(kPartFloats<D> * 4), kRawBufferWord3);
+  const int vo = (wave * NC * 16 * 64 + lane) * 4;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[c][e]), rs, vo, (c * 16 + e) * 256, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_ref), rs, tid * 4, 128 * D * 4, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_acc), rs, tid * 4, (128 * D + 256) * 4, 0);
+}
+
 template <int D, int QK, int PV, int GRAN, int MASK>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   using SM = Smem<D, PV>;
@@ -584,9 +611,105 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   const int nq = (int)(p.np / kRowsPerWG);
 
   int bh, qt;
-  item_of(blockIdx.x, (int)gridDim.x, p.bh, nq, p.light_last, bh, qt);
+  if constexpr (MASK == 0) {
+    // Unmasked: items in head-major order.  Workgroups [0, n_whole) take whole
+    // items, dealt to XCDs (workgroup i runs on XCD i % 8) in contiguous
+    // ranges so that an XCD's resident workgroups share K/V tiles in its L2.
+    // Later workgroups, dispatched last, take the pieces of the split items
+    // and leave partials for merge_split_kernel.
+    const int64_t b = blockIdx.x;
+    if (b >= p.n_whole) {
+      const int64_t c = b - p.n_whole;
+      const int64_t pos = p.n_whole + c / p.split_parts;
+      const int part = (int)(c % p.split_parts);
+      bh = (int)(pos / nq);
+      qt = (int)(pos % nq);
+      const int t0 = (int)((int64_t)part * p.nt / p.split_parts);
+      const int t1 = (int)((int64_t)(part + 1) * p.nt / p.split_parts);
+      item_tiles<D, QK, PV, GRAN, 0>(p, smem, bh, qt, t0, t1, o, m_ref, l_acc);
+      store_partial<D>(p.part + c * kPartFloats<D>, o, m_ref, l_acc);
+      return;
+    }
+    const int x = (int)(b % 8);
+    const int64_t local = b / 8, per = p.n_whole / 8, rem = p.n_whole % 8;
+    const int64_t pos = x * per + (x < rem ? x : rem) + local;
+    bh = (int)(pos / nq);
+    qt = (int)(pos % nq);
+  } else {
+    item_of(blockIdx.x, (int)gridDim.x, p.bh, nq, p.light_last, bh, qt);
+  }
   item_tiles<D, QK, PV, GRAN, MASK>(p, smem, bh, qt, 0, p.nt, o, m_ref, l_acc);
   store_rows_final<D, PV>(p, smem, bh, qt, o, m_ref, l_acc);
+}
+
+// Merges the pieces of the split items.  Block (split item, 32-row block w,
+// row group j) covers rows 8j + 4h + i (i < 4) of the block, all channels.
+// Row rho: M = max over pieces of m, L = sum 2^(m - M) * l,
+// out = sum 2^(m - M) * O / L, lse = M + log2(L) (empty rows: 0 and -inf, as
+// the attention kernel writes them).
+template <int D>
+__global__ void __launch_bounds__(256) merge_split_kernel(AttnParams p) {
+  constexpr int NC = D / 32;
+  constexpr int kMaxParts = 8;
+  const int64_t si = blockIdx.x;
+  const int w = (int)blockIdx.y, j = (int)blockIdx.z;
+  const int parts = p.split_parts;
+  const int nq = (int)(p.np / kRowsPerWG);
+  const int64_t pos = p.n_whole + si;
+  const int bh = (int)(pos / nq), qt = (int)(pos % nq);
+  const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * w;
+  if (q0 >= p.n) return;  // uniform over the block
+  const float* slots = p.part + si * parts * kPartFloats<D>;
+  __shared__ float fac[kMaxParts][8];  // rows 8j .. 8j + 7 of the block
+  const int tid = threadIdx.x;
+  if (tid < 8) {
+    const int row = 8 * j + tid;
+    float m[kMaxParts], l[kMaxParts];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q) {
+      if (q < parts) {
+        const float* sl = slots + q * kPartFloats<D> + 128 * D;
+        m[q] = sl[w * 64 + row];
+        l[q] = sl[256 + w * 64 + row] + sl[256 + w * 64 + 32 + row];
+        mx = fmaxf(mx, m[q]);
+      }
+    }
+    float tot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q) {
+      if (q < parts) {
+        m[q] = m[q] > -INFINITY ? __builtin_amdgcn_exp2f(m[q] - mx) : 0.0f;
+        tot = fmaf(m[q], l[q], tot);
+      }
+    }
+    const bool empty = !(tot > 0.0f);
+    const float inv = empty ? 0.0f : 1.0f / tot;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q)
+      if (q < parts) fac[q][tid] = m[q] * inv;
+    if (q0 + row < p.n) p.lse[(int64_t)bh * p.n + q0 + row] = empty ? -INFINITY : (mx + log2f(tot));
+  }
+  __syncthreads();
+  if (tid < NC * 64) {
+    const int c = tid >> 6, lane = tid & 63, h = lane >> 5, r = lane & 31;
+    float x[kMaxParts][4];
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        x[q][i] = q < parts ? slots[q * kPartFloats<D> + ((w * NC + c) * 16 + 4 * j + i) * 64 + lane] : 0.0f;
+    uint16_t* ob = p.out + ((int64_t)bh * p.n + q0) * D + 32 * c + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 8 * j + 4 * h + i;
+      float acc = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kMaxParts; ++q)
+        if (q < parts) acc = fmaf(fac[q][4 * h + i], x[q][i], acc);
+      if (q0 + row < p.n) ob[(int64_t)row * D] = f32_to_bf16_rne(acc);
+    }
+  }
 }
 
 // int32 QK^T of int8 codes through the attention kernel's MFMA fragments.
@@ -620,13 +743,17 @@ __global__ void __launch_bounds__(256) qk_int32_kernel(const uint8_t* __restrict
 
 template <int D, int QK, int PV, int GRAN>
 hipError_t launch_attn_g(int mask, const AttnParams& p, hipStream_t st) {
-  const dim3 grid((unsigned)(p.bh * (p.np / kRowsPerWG)));
+  const int64_t items = (int64_t)p.bh * (p.np / kRowsPerWG);
+  const int64_t n_split = mask == 0 ? items - p.n_whole : 0;
+  const dim3 grid((unsigned)(mask == 0 ? p.n_whole + n_split * p.split_parts : items));
   switch (mask) {
     case 0: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 0>), grid, dim3(256), 0, st, p); break;
     case 1: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 1>), grid, dim3(256), 0, st, p); break;
     case 2: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 2>), grid, dim3(256), 0, st, p); break;
     default: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 3>), grid, dim3(256), 0, st, p); break;
   }
+  if (n_split > 0)
+    hipLaunchKernelGGL(merge_split_kernel<D>, dim3((unsigned)n_split, 4, 4), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -667,13 +794,15 @@ hipError_t launch_qk_int32(const uint8_t* qc, const uint8_t* kc, int64_t bh, int
 }
 
 AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d) {
-  (void)h;
-  (void)d;
   const int64_t np = padded_len(n);
   const int64_t nt = (n + 63) / 64;
+  const int64_t items = b * h * (np / kRowsPerWG);
   AttnWorkspace w;
+  w.split = tail_split(items, nt);
   w.doc_off = 0;
-  w.bytes = (size_t)(b * (nt + np / 32 + np / 128)) * sizeof(int4);
+  w.part_off = ((size_t)(b * (nt + np / 32 + np / 128)) * sizeof(int4) + 255) & ~(size_t)255;
+  const int64_t pieces = w.split.parts > 1 ? (items - w.split.whole) * w.split.parts : 0;
+  w.bytes = w.part_off + (size_t)pieces * (size_t)(128 * d + 512) * sizeof(float);
   return w;
 }
 

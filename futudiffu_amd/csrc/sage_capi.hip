@@ -140,7 +140,15 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
   p.bh = (int)(b * h);
   p.nt = (int)nkv;
   p.light_last = (nq > 1 && n - (nq - 1) * 128 <= 64) ? 1 : 0;
-  if ((int64_t)p.bh * nq > 0x7fffffff)
+  // unmasked launches cut the items of the last, partial dispatch round
+  p.n_whole = (int)(b * h * nq);
+  p.split_parts = 1;
+  if (mask == 0) {
+    p.n_whole = (int)ws.split.whole;
+    p.split_parts = ws.split.parts;
+    p.part = reinterpret_cast<float*>(wsp + ws.part_off);
+  }
+  if ((int64_t)p.bh * nq + 8 * sage::kResidentWGs > 0x7fffffff)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(p.bh * nq));
   hipError_t e = sage::launch_attn(qk_kind, pv_kind, granularity, mask, p, d, (int)b, stream);
   return launch_status(e, "sage_attn_fwd");

@@ -28,7 +28,47 @@ struct AttnParams {
   int bh;          // B * H
   int nt;          // key tiles: ceil(N / 64)
   int light_last;  // last 128-row query tile holds <= 64 rows: schedule those items last
+  // unmasked launches: the items past n_whole (in schedule order) are cut into
+  // split_parts key-tile ranges whose partials a second kernel merges
+  int n_whole;
+  int split_parts;
+  float* part;  // (items - n_whole) * split_parts slots of kPartFloats<D> floats
 };
+
+// Resident workgroups of the attention kernel on MI355X: 256 CUs x 2.
+constexpr int kResidentWGs = 512;
+
+// Floats of one partial slot: O of 128 rows x D (fp32, lane order), then the
+// per-lane reference point and row-sum halves of the 4 waves.
+template <int D>
+constexpr int64_t kPartFloats = 128 * D + 2 * 256;
+
+// Tail split of an unmasked launch of n_items 128-row items of nt key tiles:
+// whole items fill complete rounds of the resident workgroups; the items of
+// the last, partial round (all items when there are fewer than one round)
+// are cut into `parts` ranges of key tiles, chosen to minimize
+// (rounds the pieces take) x (tiles per piece + 2 tiles of pipeline start).
+struct TailSplit {
+  int64_t whole;
+  int parts;
+};
+
+inline TailSplit tail_split(int64_t n_items, int64_t nt) {
+  TailSplit t{n_items, 1};
+  const int64_t rest = n_items >= kResidentWGs ? n_items % kResidentWGs : n_items;
+  if (rest == 0) return t;
+  int64_t best = (rest + kResidentWGs - 1) / kResidentWGs * (nt + 2);
+  const int pmax = (int)(nt < 8 ? nt : 8);
+  for (int p = 2; p <= pmax; ++p) {
+    const int64_t cost = (rest * p + kResidentWGs - 1) / kResidentWGs * ((nt + p - 1) / p + 2);
+    if (cost < best) {
+      best = cost;
+      t.parts = p;
+    }
+  }
+  if (t.parts > 1) t.whole = n_items - rest;
+  return t;
+}
 
 hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t* q, const uint16_t* k,
                            const uint16_t* v, int64_t bh, int64_t n, int64_t d, float fold, double* ws,
@@ -37,9 +77,11 @@ hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
 
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb, hipStream_t st);
-// Workspace of one attention call: the doc-id summaries.
+// Workspace of one attention call: the doc-id summaries, then the partial
+// slots of the tail split.
 struct AttnWorkspace {
-  size_t doc_off, bytes;
+  size_t doc_off, part_off, bytes;
+  TailSplit split;
 };
 AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d);
 size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);

@@ -44,10 +44,14 @@ def test_sizes_and_padding():
     lib = _lib.load()
     assert [lib.sage_padded_len(n) for n in (1, 128, 129, 4416)] == [128, 128, 256, 4480]
     assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 128 * 8
-    # per-batch summaries of every 64-key tile and 32- and 128-row query block
-    for b, h, n, d in ((2, 3, 200, 128), (1, 30, 4416, 128), (1, 1, 1, 64)):
+    # per-batch summaries of every 64-key tile and 32- and 128-row query block,
+    # then (256-byte aligned) fp32 slots of 128 x D + 512 floats for the pieces
+    # of the split tail: 26 items x 8 pieces at the 1x30x4416x128 headline shape
+    # (1050 items = 2 rounds of 512 + 26), 12 x 4 at 2x3x200, none for one tile
+    for b, h, n, d, pieces in ((2, 3, 200, 128, 48), (1, 30, 4416, 128, 208), (1, 1, 1, 64, 0)):
         np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
-        assert lib.sage_attn_workspace_bytes(b, h, n, d) == b * (nt + np_ // 32 + np_ // 128) * 16
+        doc = (b * (nt + np_ // 32 + np_ // 128) * 16 + 255) // 256 * 256
+        assert lib.sage_attn_workspace_bytes(b, h, n, d) == doc + pieces * (128 * d + 512) * 4
 
 
 def _quant_call(lib, **over):
@@ -96,7 +100,7 @@ def _attn_call(lib, **over):
     (dict(ws=None), 3, "workspace"),
     (dict(doc=256, ws=None), 3, "workspace"),
     (dict(ws=256, wsb=100), 3, "workspace of"),
-    (dict(doc=256, ws=264, wsb=1 << 20), 2, "workspace must be 16-byte aligned"),
+    (dict(doc=256, ws=264, wsb=1 << 24), 2, "workspace must be 16-byte aligned"),
     (dict(out=None), 1, "null"),
     (dict(pv=1, vs=None), 1, "v_scale"),
 ])
