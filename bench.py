@@ -7,11 +7,17 @@ full op call: sage_quantize_qkv (smoothing + quantization) followed by
 sage_attn_fwd, with inputs resident in HBM.
 
 Prints ONE JSON line.  ``value`` is TFLOP/s of the whole op on the
-algorithmic count 4*B*H*N^2*D; ``roofline`` is the attention kernel (the
-dominant kernel) against the dense 8-bit MFMA peak; ``quantize`` reports the
-memory-bound kernel against HBM peak; ``cpu_baseline`` times the CPU oracle
-(the reference's algorithm restated in PyTorch) on a bounded sample of the
-same workload on the host cores.
+algorithmic count 4*B*H*N^2*D; ``roofline`` is the attention kernels (the
+fused kernel plus the merge of the split tail items) against the dense 8-bit
+MFMA peak; ``quantize`` reports the memory-bound kernels against HBM peak;
+``cpu_baseline`` times the CPU oracle (the reference's algorithm restated in
+PyTorch) on a bounded sample of the same workload on the host cores.
+
+``--all-configs`` instead prints one JSON line per benchmark configuration
+(the CPU plumbing case, 512x512, both 1280x832 variants, the packed
+mixed-resolution batch with the reference tile mask and with exact document
+ids, the k-tuple batch with key padding), each with its throughput, roofline
+fraction and CPU baseline.
 """
 
 from __future__ import annotations
@@ -50,7 +56,30 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device copy of MIB MiB "
                          "--steps times (scales the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--all-configs", action="store_true",
+                    help="one JSON line per benchmark configuration instead of the headline line")
+    ap.add_argument("--cases", default="",
+                    help="comma-separated subset of the --all-configs cases")
     return ap.parse_args()
+
+
+# Benchmark configurations: the CPU plumbing case, the 512x512 and 1280x832
+# single-image shapes, the packed mixed-resolution batch (1280 + 1216 + 4416
+# tokens) with the reference 128x64 tile mask and with exact document ids, and
+# the k-tuple batch of four 1024x1024 samples with per-sample text padding.
+CASES = {
+    "plumbing_b1h4n256d64": dict(B=1, H=4, N=256, D=64, qk="int8", pv="bf16", gran="block64"),
+    "dit512_b1h30n1280": dict(B=1, H=30, N=1280, D=128, qk="int8", pv="fp8", gran="token"),
+    "dit1280x832_int8fp8": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="fp8", gran="token"),
+    "dit1280x832_fp8bf16": dict(B=1, H=30, N=4416, D=128, qk="fp8", pv="bf16", gran="token"),
+    "packed_tilemask": dict(B=1, H=30, N=6912, D=128, qk="int8", pv="fp8", gran="token",
+                            segments=[1280, 1216, 4416], mask="tile"),
+    "packed_docids": dict(B=1, H=30, N=6912, D=128, qk="int8", pv="fp8", gran="token",
+                          segments=[1280, 1216, 4416], mask="doc"),
+    "ktuple_b4n4352_keypad": dict(B=4, H=30, N=4352, D=128, qk="int8", pv="fp8", gran="token",
+                                  mask="keypad", text=256),
+}
+PEAK_MIXED_TFLOPS = 2.0 / (1.0 / PEAK_8BIT_TFLOPS + 1.0 / PEAK_BF16_TFLOPS)  # fp8 QK + bf16 PV
 
 
 def quant_bytes(B, H, N, D, pv, gran):
@@ -149,6 +178,142 @@ def copy_calibration(args):
                       "launches": args.steps}), flush=True)
 
 
+def _case_inputs(c, dev, seed=0):
+    """Seeded q/k/v of a case (K with a per-channel N(0, 2) offset), its masks,
+    and its algorithmic FLOP count (visible query-key pairs x 4D)."""
+    B, H, N, D = c["B"], c["H"], c["N"], c["D"]
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    q = torch.randn(B, H, N, D, generator=g).bfloat16()
+    k = (torch.randn(B, H, N, D, generator=g) + 2.0 * torch.randn(B, H, 1, D, generator=g)).bfloat16()
+    v = torch.randn(B, H, N, D, generator=g).bfloat16()
+    mask = c.get("mask")
+    block_mask = doc = None
+    flop = 4.0 * B * H * N * N * D
+    extra = {}
+    if mask in ("tile", "doc"):
+        from futudiffu_amd import block_mask as BM
+        segs = c["segments"]
+        flop = 4.0 * B * H * D * sum(x * x for x in segs)
+        extra["flop_dense"] = 4.0 * B * H * N * N * D
+        if mask == "tile":
+            block_mask = BM.build_block_mask(segs, N, device="cpu")
+            extra["tile_skip_efficiency"] = round(float(block_mask.float().mean()), 4)
+            extra["active_tiles"] = int(block_mask.sum())
+            extra["total_tiles"] = int(block_mask.numel())
+        else:
+            doc = BM.build_doc_ids(segs, N, device="cpu", batch=B)
+    elif mask == "keypad":
+        # text first: sample b keeps L_b ~ U[32, 256] of its 256 text slots, the
+        # rest of the text slots are padding keys; all image tokens are valid
+        gl = torch.Generator(device="cpu").manual_seed(seed + 1)
+        lens = torch.randint(32, c["text"] + 1, (B,), generator=gl)
+        valid = torch.ones(B, N, dtype=torch.bool)
+        for b in range(B):
+            valid[b, int(lens[b]):c["text"]] = False
+        doc = torch.where(valid, 0, -1).to(torch.int32)
+        nvalid = valid.sum(dim=1).double()
+        # every query (padded ones included) attends the valid keys of its sample
+        flop = float(4.0 * H * D * N * nvalid.sum())
+        extra["flop_dense"] = 4.0 * B * H * N * N * D
+        extra["text_lengths"] = [int(x) for x in lens]
+    return q, k, v, block_mask, doc, flop, extra
+
+
+def _cpu_case(c, q, k, v, block_mask, doc, flop, budget_s):
+    """CPU oracle and CPU SDPA on one head of batch 0 of the case (bounded)."""
+    from oracle import sage_oracle as O
+    N = c["N"]
+    q1, k1, v1 = q[:1, :1], k[:1, :1], v[:1, :1]
+    d1 = None if doc is None else doc[:1]
+    t0 = time.perf_counter()
+    O.sage_forward(q1, k1, v1, None, c["qk"], c["pv"], c["gran"], True, block_mask, d1)
+    per_head = time.perf_counter() - t0
+    reps = 0
+    if per_head < budget_s / 2:
+        reps = max(1, min(4, int(budget_s / per_head) - 1))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            O.sage_forward(q1, k1, v1, None, c["qk"], c["pv"], c["gran"], True, block_mask, d1)
+        per_head = (time.perf_counter() - t0) / reps
+    heads = c["B"] * c["H"]
+    vis = None
+    if block_mask is not None:
+        vis = O.tile_mask_visibility(block_mask, 1, N)
+    if d1 is not None:
+        dv = O.doc_visibility(d1.to(torch.int64))
+        vis = dv if vis is None else vis & dv
+    t0 = time.perf_counter()
+    torch.nn.functional.scaled_dot_product_attention(q1, k1, v1, attn_mask=None if vis is None else vis[:, None])
+    sdpa = time.perf_counter() - t0
+    return {
+        "value": round(flop / heads / per_head / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle (torch CPU emulation of the reference quantized attention) on {reps + 1} run(s) "
+                   f"of one head (batch 0, head 0) of this case; {per_head * 1e3:.1f} ms/head, "
+                   f"throughput on that head's share of the FLOPs"),
+        "sdpa_bf16_cpu_ms_per_head": round(sdpa * 1e3, 3),
+        "cpu_model": _cpu_model(),
+    }
+
+
+def all_configs(args):
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from futudiffu_amd import sage_attention as SA
+    dev = torch.device("cuda:0")
+    names = [x for x in args.cases.split(",") if x] or list(CASES)
+    for name in names:
+        c = CASES[name]
+        B, H, N, D = c["B"], c["H"], c["N"], c["D"]
+        print(f"# case {name}", file=sys.stderr, flush=True)
+        q, k, v, bm, doc, flop, extra = _case_inputs(c, dev)
+        qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+        bmd = None if bm is None else bm.to(dev)
+        docd = None if doc is None else doc.to(dev)
+        sm = 1.0 / math.sqrt(D)
+
+        def step(ev=None):
+            if ev is not None:
+                ev[0].record()
+            qz = SA.quantize_qkv(qd, kd, vd, sm, qk=c["qk"], pv=c["pv"], granularity=c["gran"])
+            if ev is not None:
+                ev[1].record()
+            SA.attn_from_quantized(qz, B, H, block_mask=bmd, doc_ids=docd)
+            if ev is not None:
+                ev[2].record()
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        for i in range(args.steps):
+            step(evs[i])
+        torch.cuda.synchronize()
+        a_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+        q_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+        tf = flop / (a_ms * 1e-3) / 1e12
+        qb = quant_bytes(B, H, N, D, c["pv"], c["gran"])
+        line = {
+            "case": name,
+            "config": {k2: v2 for k2, v2 in c.items()},
+            "attn_ms": round(a_ms, 5),
+            "attn_tflops": round(tf, 2),
+            "flop": flop,
+            "roofline": {"bound": "mfma", "peak": PEAK_8BIT_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_8BIT_TFLOPS, 4)},
+            "quantize": {"ms": round(q_ms, 5), "GB/s": round(qb / (q_ms * 1e-3) / 1e9, 1),
+                         "frac_of_hbm_peak": round(qb / (q_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "op_ms": round(a_ms + q_ms, 5),
+        }
+        if c["pv"] == "bf16" and c["qk"] == "fp8":
+            line["roofline"]["frac_of_mixed_fp8_bf16_peak"] = round(tf / PEAK_MIXED_TFLOPS, 4)
+        line.update(extra)
+        if not args.no_cpu_baseline:
+            line["cpu_baseline"] = _cpu_case(c, q, k, v, bm, doc, flop, args.cpu_seconds)
+        print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -160,6 +325,9 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args)
+        return
+    if args.all_configs:
+        all_configs(args)
         return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from futudiffu_amd import sage_attention as SA
@@ -229,7 +397,7 @@ def main():
         "pct_of_fp8_peak": round(100.0 * flop / (ms_per_step * 1e-3) / 1e12 / PEAK_8BIT_TFLOPS, 2),
         "roofline": {
             "bound": "mfma",
-            "kernel": "attn_fwd_kernel",
+            "kernel": "attn_fwd_kernel + merge_split_kernel",
             "achieved": round(attn_tflops, 3),
             "peak": peak,
             "unit": "TFLOP/s",
