@@ -186,6 +186,26 @@ __device__ __forceinline__ void qk_half(const uint8_t* sb, const i32x4* qf, int 
   }
 }
 
+// Both 32-key halves of the next S^T as two interleaved MFMA chains.
+template <int D, int QK>
+__device__ __forceinline__ void qk_both(const uint8_t* sb, const i32x4* qf, int lane, typename SAccT<QK>::type& a0,
+                                        typename SAccT<QK>::type& a1) {
+  constexpr int NC = D / 32;
+  const i32x4* kl = reinterpret_cast<const i32x4*>(sb);
+  if constexpr (QK == kQK_INT8) {
+    a0 = i32x16{0};
+    a1 = i32x16{0};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(0 * NC + c) * 64 + lane], qf[c], a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(1 * NC + c) * 64 + lane], qf[c], a1, 0, 0, 0);
+    }
+  } else {
+    qk_half<D, QK>(sb, qf, lane, 0, a0);
+    qk_half<D, QK>(sb, qf, lane, 1, a1);
+  }
+}
+
 // Per-row values for the O fragment: lane (h, r) holds rows 8j + 4h + i,
 // element 4j + i.  Lanes h = 0 publish their row's value in the wave's
 // 32-float exchange; every lane then reads four broadcast float4s.
@@ -207,8 +227,9 @@ __device__ __forceinline__ void rows_of(float* xrow, float v, int h, int r, floa
 }
 
 // The per-tile work of one wave, as straight-line code for the scheduler:
-// scores of tile t from s0/s1, the next tile's S^T into s0/s1 (issued early so
-// the matrix cores overlap this tile's vector work), online softmax, P.V.
+// scores of tile t from s0/s1, the next tile's S^T into s0/s1 (both halves
+// issued first, as two interleaved MFMA chains, so the matrix cores overlap
+// this tile's vector work), online softmax, P.V.
 // MASKED selects the per-token document-id visibility test.
 template <int D, int QK, int PV, int GRAN, int MASK, bool MASKED>
 __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_next, const i32x4* qf, int lane,
@@ -236,7 +257,7 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
         for (int i = 0; i < 4; ++i) u[b][4 * j + i] = fmaf((float)(b ? s1 : s0)[4 * j + i], kd4[i], kb4[i]);
       }
   }
-  qk_half<D, QK>(sb_next, qf, lane, 0, s0);
+  qk_both<D, QK>(sb_next, qf, lane, s0, s1);
   if constexpr (MASKED) {
     // per-token document ids: key visible iff doc[key] >= 0 and (doc[q] == doc[key] or doc[q] < 0)
     const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
@@ -287,7 +308,6 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
 #pragma unroll
       for (int e = 0; e < 16; ++e) o[c][e] *= arow[e];
   }
-  qk_half<D, QK>(sb_next, qf, lane, 1, s1);
 
   if constexpr (PV == kPV_FP8) {
     // reference per-(row, 64-key block) P codes: e = 2^(s - bm) * 448; the
@@ -497,8 +517,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
   __syncthreads();
   SAcc s0, s1;  // S^T of the tile about to be consumed
   if (t < t_end && wave_live) {
-    qk_half<D, QK>(smem, qf, lane, 0, s0);
-    qk_half<D, QK>(smem, qf, lane, 1, s1);
+    qk_both<D, QK>(smem, qf, lane, s0, s1);
   }
 
   int stage = 0;
@@ -517,8 +536,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
     else if (cls == 1)
       tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq);
     else if (wave_live && t1 < t_end) {
-      qk_half<D, QK>(sb_next, qf, lane, 0, s0);
-      qk_half<D, QK>(sb_next, qf, lane, 1, s1);
+      qk_both<D, QK>(sb_next, qf, lane, s0, s1);
     }
 
     // ---- hand over: tile t2 into the stage tile t - 1 used ----------------------
