@@ -47,8 +47,9 @@ def test_sizes_and_padding():
     # per-batch summaries of every 64-key tile and 32- and 128-row query block,
     # then (256-byte aligned) fp32 slots of 128 x D + 512 floats for the pieces
     # of the split tail: 26 items x 8 pieces at the 1x30x4416x128 headline shape
-    # (1050 items = 2 rounds of 512 + 26), 12 x 4 at 2x3x200, none for one tile
-    for b, h, n, d, pieces in ((2, 3, 200, 128, 48), (1, 30, 4416, 128, 208), (1, 1, 1, 64, 0)):
+    # (1050 items = 2 rounds of 512 + 26), none below one round of 512 items
+    for b, h, n, d, pieces in ((2, 3, 200, 128, 0), (1, 30, 4416, 128, 208), (1, 1, 1, 64, 0),
+                               (1, 30, 1280, 128, 0), (2, 30, 4416, 128, 52 * 8)):
         np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
         doc = (b * (nt + np_ // 32 + np_ // 128) * 16 + 255) // 256 * 256
         assert lib.sage_attn_workspace_bytes(b, h, n, d) == doc + pieces * (128 * d + 512) * 4

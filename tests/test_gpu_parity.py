@@ -19,7 +19,10 @@ pytestmark = pytest.mark.gpu
 TOL_MAXABS = 2e-2      # output max-abs vs the reference-scheme emulation
 TOL_COS = 0.999        # output cosine vs the reference-scheme emulation
 TIGHT_COS = 0.99999    # vs the emulation of the kernel's own P scaling
-TIGHT_MAXABS = 4e-3
+# v_exp_f32 and the oracle's exp2 differ by ulps, which now and then moves a P
+# value across an e4m3 rounding boundary (one code step, 1/16 to 1/8 of that
+# P); over millions of outputs the largest such flip reaches ~4e-3.
+TIGHT_MAXABS = 8e-3
 LSE_TOL = 2e-3         # log2 units
 
 
@@ -126,9 +129,12 @@ def _compare(out, lse, q, k, v, qk, pv, gran, block_mask=None, doc_ids=None, smo
             st, _, _ = O.sage_forward(q, k, v, None, qk, pv, gran, smooth, block_mask, doc_ids,
                                       p_scheme="static", tau=8.0)
         tcos = O.cosine(out, st)
-        tmax = (out - st.float()).abs().max().item()
+        terr = (out - st.float()).abs()
+        tmax = terr.max().item()
+        where = [int(i) for i in torch.nonzero(terr == tmax)[0]]
         assert tcos >= TIGHT_COS, f"cosine {tcos:.7f} vs kernel-scheme emulation"
-        assert tmax <= TIGHT_MAXABS, f"max-abs {tmax:.4g} vs kernel-scheme emulation"
+        assert tmax <= TIGHT_MAXABS, (f"max-abs {tmax:.4g} vs kernel-scheme emulation at [b, h, n, d] = {where} "
+                                      f"(value {float(st.float().flatten()[terr.flatten().argmax()]):.4f})")
     return maxabs, cos
 
 
@@ -256,3 +262,16 @@ def test_headline_schedule_consistency(cuda, qk, pv):
     assert O.cosine(a.cpu(), b.cpu()) >= 0.99999
     assert (a.float() - b.float()).abs().max().item() <= 4e-3
     assert (la - lb).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("qk,pv,D", [("int8", "fp8", 128), ("fp8", "bf16", 64)])
+def test_split_tail_matches_oracle(cuda, qk, pv, D):
+    """520 query-tile items (2 x 130 heads x 2 tiles) fill one round of 512
+    workgroups and leave 8 items that are cut into 4 key-tile pieces each and
+    merged by the second kernel."""
+    SA = _sa()
+    B, H, N = 2, 130, 256
+    q, k, v = O.make_inputs(B, H, N, D, seed=43 + D)
+    out, lse = SA.sage_forward(q.to(cuda), k.to(cuda), v.to(cuda), qk=qk, pv=pv)
+    torch.cuda.synchronize()
+    _compare(out, lse, q, k, v, qk, pv, "token")
