@@ -78,6 +78,10 @@ CASES = {
                           segments=[1280, 1216, 4416], mask="doc"),
     "ktuple_b4n4352_keypad": dict(B=4, H=30, N=4352, D=128, qk="int8", pv="fp8", gran="token",
                                   mask="keypad", text=256),
+    # the 1280x832 shape with the output stored as the out-projection's
+    # [B, N, H*D] input, timed against [B, H, N, D] + the caller's transpose copy
+    "dit1280x832_int8fp8_outproj": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="fp8", gran="token",
+                                        out="bnhd"),
 }
 PEAK_MIXED_TFLOPS = 2.0 / (1.0 / PEAK_8BIT_TFLOPS + 1.0 / PEAK_BF16_TFLOPS)  # fp8 QK + bf16 PV
 
@@ -272,26 +276,37 @@ def all_configs(args):
         bmd = None if bm is None else bm.to(dev)
         docd = None if doc is None else doc.to(dev)
         sm = 1.0 / math.sqrt(D)
+        layout = c.get("out", "bhnd")
 
-        def step(ev=None):
+        def step(ev=None, out_layout=layout, merge_heads=False):
             if ev is not None:
                 ev[0].record()
             qz = SA.quantize_qkv(qd, kd, vd, sm, qk=c["qk"], pv=c["pv"], granularity=c["gran"])
             if ev is not None:
                 ev[1].record()
-            SA.attn_from_quantized(qz, B, H, block_mask=bmd, doc_ids=docd)
+            out, _ = SA.attn_from_quantized(qz, B, H, block_mask=bmd, doc_ids=docd, out_layout=out_layout)
+            if merge_heads:  # the caller's copy into the out-projection layout (transformer.py:471)
+                out.transpose(1, 2).reshape(B, -1, H * D)
             if ev is not None:
                 ev[2].record()
 
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-        for i in range(args.steps):
-            step(evs[i])
-        torch.cuda.synchronize()
-        a_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
-        q_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+        def timed(**kw):
+            for _ in range(args.warmup):
+                step(**kw)
+            torch.cuda.synchronize()
+            evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+            for i in range(args.steps):
+                step(evs[i], **kw)
+            torch.cuda.synchronize()
+            return (sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps,
+                    sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps)
+
+        a_ms, q_ms = timed()
+        if layout == "bnhd":
+            sep_ms, _ = timed(out_layout="bhnd", merge_heads=True)
+            extra["outproj_input"] = {"fused_bnhd_store_ms": round(a_ms, 5),
+                                      "bhnd_store_plus_transpose_copy_ms": round(sep_ms, 5),
+                                      "saved_ms": round(sep_ms - a_ms, 5)}
         tf = flop / (a_ms * 1e-3) / 1e12
         qb = quant_bytes(B, H, N, D, c["pv"], c["gran"])
         line = {

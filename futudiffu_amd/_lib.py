@@ -28,7 +28,7 @@ SIGNATURES = {
     "sage_attn_workspace_bytes": (_c.c_size_t, [_I64, _I64, _I64, _I64]),
     "sage_attn_fwd": (_c.c_int, [
         _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_int,
-        _P, _I64, _I64, _I64, _P, _P, _c.c_size_t, _P, _P, _P]),
+        _P, _I64, _I64, _I64, _P, _P, _c.c_size_t, _P, _c.c_int, _P, _P]),
     "sage_qk_int32": (_c.c_int, [_P, _P, _I64, _I64, _I64, _P, _P]),
 }
 
@@ -50,7 +50,7 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
-            if lib.sage_abi_version() != 2:
+            if lib.sage_abi_version() != 3:
                 raise RuntimeError("libsage_mi355x.so ABI version mismatch")
             _lib = lib
         return _lib

@@ -12,7 +12,10 @@ production kernel it replaces (sage_attention.py:521-529); the unmasked op uses
 the ``configure_sage`` selection (sage_attention.py:271-341).
 
 ``futudiffu_ii::sage_attn_ext`` exposes every variant as op arguments
-(qk, pv, granularity, smoothing, optional tile mask, optional exact doc ids).
+(qk, pv, granularity, smoothing, optional tile mask, optional exact doc ids,
+output layout).  ``futudiffu_ii::sage_attn_masked_merged_heads`` is
+``sage_attn_masked`` with the output already in the ``[B, N, H*D]`` layout of
+the out-projection that follows it (transformer.py:471).
 
 Backward is not part of this forward-only build: the ops register an autograd
 formula that raises, so a training graph fails loudly instead of silently
@@ -25,7 +28,12 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from .sage_attention import sage_attn_forward_masked_with_lse, sage_attn_forward_with_lse, sage_forward
+from .sage_attention import (
+    sage_attn_forward_masked_merged_heads,
+    sage_attn_forward_masked_with_lse,
+    sage_attn_forward_with_lse,
+    sage_forward,
+)
 
 
 def _fake_out(q: Tensor) -> tuple[Tensor, Tensor]:
@@ -74,15 +82,41 @@ sage_attn_op.register_autograd(_no_backward, setup_context=_setup_context)
 @torch.library.custom_op("futudiffu_ii::sage_attn_ext", mutates_args=())
 def sage_attn_ext_op(q: Tensor, k: Tensor, v: Tensor, block_mask: Tensor | None, doc_ids: Tensor | None,
                      sm_scale: float, qk: str, pv: str, granularity: str,
-                     smooth_k: bool) -> tuple[Tensor, Tensor]:
+                     smooth_k: bool, out_layout: str = "bhnd") -> tuple[Tensor, Tensor]:
     out, lse = sage_forward(q, k, v, sm_scale, block_mask=block_mask, doc_ids=doc_ids, qk=qk, pv=pv,
-                            granularity=granularity, smooth_k=smooth_k)
+                            granularity=granularity, smooth_k=smooth_k, out_layout=out_layout)
     return out, lse
 
 
 @sage_attn_ext_op.register_fake
-def _fake_ext(q, k, v, block_mask, doc_ids, sm_scale, qk, pv, granularity, smooth_k):
+def _fake_ext(q, k, v, block_mask, doc_ids, sm_scale, qk, pv, granularity, smooth_k, out_layout="bhnd"):
+    if out_layout == "bnhd":
+        return _fake_merged_heads(q)
     return _fake_out(q)
 
 
 sage_attn_ext_op.register_autograd(_no_backward, setup_context=_setup_context)
+
+
+def _fake_merged_heads(q: Tensor) -> tuple[Tensor, Tensor]:
+    B, H, N, D = q.shape
+    return q.new_empty(B, N, H * D), q.new_empty(B * H, N, dtype=torch.float32)
+
+
+# JointAttention.forward (transformer.py:467-471) calls sage_attn_masked and
+# then out.transpose(1, 2).reshape(b, -1, H*D) for its out-projection.  This op
+# returns that [B, N, H*D] tensor directly (the kernel stores rows in that
+# layout), bit-identical to the transposed output of sage_attn_masked.
+@torch.library.custom_op("futudiffu_ii::sage_attn_masked_merged_heads", mutates_args=())
+def sage_attn_masked_merged_heads_op(q: Tensor, k: Tensor, v: Tensor, block_mask: Tensor,
+                                     sm_scale: float) -> tuple[Tensor, Tensor]:
+    out, lse = sage_attn_forward_masked_merged_heads(q, k, v, block_mask, sm_scale)
+    return out, lse
+
+
+@sage_attn_masked_merged_heads_op.register_fake
+def _fake_fwd_merged(q, k, v, block_mask, sm_scale):
+    return _fake_merged_heads(q)
+
+
+sage_attn_masked_merged_heads_op.register_autograd(_no_backward, setup_context=_setup_context)

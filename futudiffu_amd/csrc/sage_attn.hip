@@ -587,16 +587,21 @@ __device__ __forceinline__ void store_rows_final(const AttnParams& p, uint8_t* s
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
   __builtin_amdgcn_wave_barrier();
-  // 16-byte stores through a buffer resource that ends at row N: the hardware
-  // drops the stores of rows past N
+  // 16-byte stores through a buffer resource that ends after the last row
+  // below N: the hardware drops the stores of rows past N.  The whole offset
+  // goes in the vector operand, the part the range check covers.
   const int rows = p.n - q0 < 32 ? (int)(p.n - q0) : 32;
-  const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(p.out + ((int64_t)bh * p.n + q0) * D, 0, rows * D * 2, kRawBufferWord3);
+  const int bh_b = bh / p.h, bh_h = bh - bh_b * p.h;
+  const int rs_bytes = (int)(p.out_rs * 2);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      p.out + bh_b * p.out_bs + bh_h * p.out_hs + q0 * p.out_rs, 0, (rows - 1) * rs_bytes + D * 2, kRawBufferWord3);
+  constexpr int kRowsPerStore = 16 * 64 / (2 * D);  // rows one 64-lane 16-byte store covers
+  const int voff = (lane * 16 / (2 * D)) * rs_bytes + (lane * 16) % (2 * D);
 #pragma unroll
   for (int i = 0; i < 32 * D * 2 / (16 * 64); ++i) {
     const int off = (lane + 64 * i) * 16;  // row-major bytes: row off / (2D), column (off % 2D) / 2
     const i32x4 v = *reinterpret_cast<const i32x4*>(reinterpret_cast<const uint8_t*>(ep) + off);
-    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, voff + i * kRowsPerStore * rs_bytes, 0, 0);
   }
 }
 
@@ -717,7 +722,8 @@ __global__ void __launch_bounds__(256) merge_split_kernel(AttnParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         x[q][i] = q < parts ? slots[q * kPartFloats<D> + ((w * NC + c) * 16 + 4 * j + i) * 64 + lane] : 0.0f;
-    uint16_t* ob = p.out + ((int64_t)bh * p.n + q0) * D + 32 * c + r;
+    const int bh_b = bh / p.h, bh_h = bh - bh_b * p.h;
+    uint16_t* ob = p.out + bh_b * p.out_bs + bh_h * p.out_hs + q0 * p.out_rs + 32 * c + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 8 * j + 4 * h + i;
@@ -725,7 +731,7 @@ __global__ void __launch_bounds__(256) merge_split_kernel(AttnParams p) {
 #pragma unroll
       for (int q = 0; q < kMaxParts; ++q)
         if (q < parts) acc = fmaf(fac[q][4 * h + i], x[q][i], acc);
-      if (q0 + row < p.n) ob[(int64_t)row * D] = f32_to_bf16_rne(acc);
+      if (q0 + row < p.n) ob[row * p.out_rs] = f32_to_bf16_rne(acc);
     }
   }
 }

@@ -87,7 +87,7 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
                   const void* v_in, const float* v_scale, int64_t b, int64_t h, int64_t n, int64_t d, int qk_kind,
                   int pv_kind, int granularity, const uint8_t* tile_mask, int64_t mask_stride_z, int64_t mask_nq,
                   int64_t mask_nkv, const int32_t* doc_ids, void* workspace, size_t workspace_bytes, void* out,
-                  float* lse, hipStream_t stream) {
+                  int out_layout, float* lse, hipStream_t stream) {
   if (b <= 0 || h <= 0) return fail(SAGE_ERR_ARG, "b=%lld and h=%lld must be positive", (long long)b, (long long)h);
   int st = check_common(b * h, n, d, qk_kind, pv_kind, granularity);
   if (st) return st;
@@ -98,6 +98,10 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
   for (const void* p : ptrs)
     if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
   if (v_scale && !aligned16(v_scale)) return fail(SAGE_ERR_ALIGN, "v_scale must be 16-byte aligned");
+  if (out_layout != SAGE_OUT_BHND && out_layout != SAGE_OUT_BNHD)
+    return fail(SAGE_ERR_ARG, "out_layout must be 0 ([B,H,N,D]) or 1 ([B,N,H,D]), got %d", out_layout);
+  // The epilogue addresses 32 output rows of one head in 32-bit byte offsets:
+  // at most 32 * h*d*2 bytes, under 2^31 since b*h <= 65535 and d <= 128.
   const int64_t nq = (n + 127) / 128, nkv = (n + 63) / 64;
   int mask = 0;
   if (tile_mask) {
@@ -133,6 +137,15 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
   p.mask_nkv = mask_nkv;
   p.doc = doc_ids;
   p.out = static_cast<uint16_t*>(out);
+  if (out_layout == SAGE_OUT_BNHD) {
+    p.out_bs = n * h * d;
+    p.out_hs = d;
+    p.out_rs = h * d;
+  } else {
+    p.out_bs = h * n * d;
+    p.out_hs = n * d;
+    p.out_rs = d;
+  }
   p.lse = lse;
   p.n = n;
   p.np = sage::padded_len(n);

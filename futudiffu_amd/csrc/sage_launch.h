@@ -21,6 +21,9 @@ struct AttnParams {
   const int4* q_sum;     // [B][Np/32] same over queries < N
   const int4* q_sum128;  // [B][Np/128] same over queries < N
   uint16_t* out;
+  // element strides of out per batch, head and row: [B,H,N,D] is
+  // (H*N*D, N*D, D), [B,N,H,D] is (N*H*D, D, H*D)
+  int64_t out_bs, out_hs, out_rs;
   float* lse;
   int64_t n;
   int64_t np;

@@ -45,6 +45,10 @@ _SAGE_PV_QUANT = "bf16"
 _QK = {"int8": 0, "fp8": 1}
 _PV = {"bf16": 0, "fp8": 1}
 _GRAN = {"token": 0, "block64": 1}
+# Output layouts: "bhnd" is the reference op's [B, H, N, D]; "bnhd" is
+# [B, N, H*D], the out-projection input JointAttention builds with
+# out.transpose(1, 2).reshape(b, -1, H*D) (transformer.py:471)
+_LAYOUT = {"bhnd": 0, "bnhd": 1}
 
 
 def configure_sage(*, smooth_k: bool = True, qk_quant: str = "fp8", pv_quant: str = "bf16") -> None:
@@ -159,11 +163,18 @@ def _norm_mask(block_mask: Tensor | None, BH: int, N: int, device) -> tuple[Tens
 
 def attn_from_quantized(qz: SageQuantized, B: int, H: int, *, block_mask: Tensor | None = None,
                         doc_ids: Tensor | None = None, out: Tensor | None = None,
-                        lse: Tensor | None = None) -> tuple[Tensor, Tensor]:
-    """Run the fused attention kernel on quantized operands; returns (out, lse)."""
+                        lse: Tensor | None = None, out_layout: str = "bhnd") -> tuple[Tensor, Tensor]:
+    """Run the fused attention kernel on quantized operands; returns (out, lse).
+
+    ``out`` is ``[B, H, N, D]`` for ``out_layout="bhnd"`` and ``[B, N, H*D]``
+    for ``"bnhd"`` (same values, written in the out-projection's layout).
+    """
+    if out_layout not in _LAYOUT:
+        raise ValueError(f"out_layout must be one of {sorted(_LAYOUT)}, got {out_layout!r}")
     lib = _lib.load()
     BH, N, D = B * H, qz.n, qz.d
     dev = qz.q_codes.device
+    out_shape = (B, H, N, D) if out_layout == "bhnd" else (B, N, H * D)
     bm, stride_z, nq, nkv = _norm_mask(block_mask, BH, N, dev)
     if doc_ids is not None:
         if doc_ids.shape != (B, N):
@@ -172,22 +183,31 @@ def attn_from_quantized(qz: SageQuantized, B: int, H: int, *, block_mask: Tensor
     wsb = int(lib.sage_attn_workspace_bytes(B, H, N, D))
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     if out is None:
-        out = torch.empty(B, H, N, D, dtype=torch.bfloat16, device=dev)
+        out = torch.empty(out_shape, dtype=torch.bfloat16, device=dev)
+    elif (tuple(out.shape) != out_shape or out.dtype != torch.bfloat16 or not out.is_contiguous()
+          or out.device != dev):
+        raise ValueError(f"out must be a contiguous bf16 {list(out_shape)} tensor on {dev}")
     if lse is None:
         lse = torch.empty(BH, N, dtype=torch.float32, device=dev)
+    elif tuple(lse.shape) != (BH, N) or lse.dtype != torch.float32 or not lse.is_contiguous() or lse.device != dev:
+        raise ValueError(f"lse must be a contiguous fp32 [{BH}, {N}] tensor on {dev}")
     _lib.check(lib.sage_attn_fwd(
         qz.q_codes.data_ptr(), qz.q_scale.data_ptr(), qz.k_codes.data_ptr(), qz.k_scale.data_ptr(),
         qz.v_op.data_ptr(), _ptr(qz.v_scale), B, H, N, D, _QK[qz.qk], _PV[qz.pv], _GRAN[qz.granularity],
-        _ptr(bm), stride_z, nq, nkv, _ptr(doc_ids), _ptr(ws), wsb, out.data_ptr(), lse.data_ptr(),
-        _stream_handle(dev)))
+        _ptr(bm), stride_z, nq, nkv, _ptr(doc_ids), _ptr(ws), wsb, out.data_ptr(), _LAYOUT[out_layout],
+        lse.data_ptr(), _stream_handle(dev)))
     return out, lse
 
 
 def sage_forward(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None, *,
                  block_mask: Tensor | None = None, doc_ids: Tensor | None = None,
                  qk: str | None = None, pv: str | None = None, granularity: str = "token",
-                 smooth_k: bool | None = None) -> tuple[Tensor, Tensor]:
-    """Sage forward with explicit variant selection; returns ``(out [B,H,N,D], lse [B*H,N])``."""
+                 smooth_k: bool | None = None, out_layout: str = "bhnd") -> tuple[Tensor, Tensor]:
+    """Sage forward with explicit variant selection; returns ``(out, lse [B*H,N])``.
+
+    ``out`` is ``[B, H, N, D]`` (``out_layout="bhnd"``, the reference op's
+    output) or ``[B, N, H*D]`` (``"bnhd"``, the out-projection's input).
+    """
     B, H, N, D = _check_inputs(q, k, v)
     qk = _SAGE_QK_QUANT if qk is None else qk
     pv = _SAGE_PV_QUANT if pv is None else pv
@@ -198,8 +218,10 @@ def sage_forward(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None,
         raise ValueError(f"Unknown pv_quant: {pv!r}")
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
+    if out_layout not in _LAYOUT:
+        raise ValueError(f"out_layout must be one of {sorted(_LAYOUT)}, got {out_layout!r}")
     qz = quantize_qkv(q, k, v, sm_scale, qk=qk, pv=pv, granularity=granularity, smooth_k=smooth_k)
-    return attn_from_quantized(qz, B, H, block_mask=block_mask, doc_ids=doc_ids)
+    return attn_from_quantized(qz, B, H, block_mask=block_mask, doc_ids=doc_ids, out_layout=out_layout)
 
 
 def sage_attn_forward(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None) -> Tensor:
@@ -230,6 +252,21 @@ def sage_attn_forward_masked_with_lse(q: Tensor, k: Tensor, v: Tensor, block_mas
     (sage_attention.py:461-531, hard-wired at :521-529)."""
     return sage_forward(q, k, v, sm_scale, block_mask=block_mask, doc_ids=doc_ids, qk=qk, pv=pv,
                         granularity=granularity)
+
+
+def sage_attn_forward_masked_merged_heads(q: Tensor, k: Tensor, v: Tensor, block_mask: Tensor,
+                                          sm_scale: float | None = None, *, qk: str = "int8",
+                                          pv: str = "bf16", granularity: str = "token",
+                                          doc_ids: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """``sage_attn_forward_masked_with_lse`` with the output in ``[B, N, H*D]``.
+
+    Bit-identical to ``out.transpose(1, 2).reshape(B, N, H*D)`` of the masked
+    forward, which JointAttention.forward computes before its out-projection
+    (transformer.py:467-471); the kernel writes that layout directly, so the
+    transpose copy disappears.
+    """
+    return sage_forward(q, k, v, sm_scale, block_mask=block_mask, doc_ids=doc_ids, qk=qk, pv=pv,
+                        granularity=granularity, out_layout="bnhd")
 
 
 def qk_int32(q_codes: Tensor, k_codes: Tensor, bh: int, n: int, d: int) -> Tensor:

@@ -40,8 +40,11 @@
  *   v_scale      fp8 PV only: fp32 [BH, Np/64, D], one scale per (64-token
  *                block, channel) (sage_kernels.py:1143-1148).
  *   k_mean       bf16 [BH, D] smoothing mean (written when smooth_k != 0).
- *   out          bf16 [BH, N, D] contiguous.
- *   lse          fp32 [BH, N], log2 domain: m + log2(l) in sm_scale*log2(e)
+ *   out          bf16 [B, H, N, D] contiguous (out_layout 0), or
+ *                bf16 [B, N, H, D] contiguous (out_layout 1): the
+ *                [B, N, H*D] input of the out-projection, written without the
+ *                caller's transpose copy (transformer.py:471).
+ *   lse        fp32 [BH, N], log2 domain: m + log2(l) in sm_scale*log2(e)
  *                units (sage_kernels.py:1468-1471).  Rows that see no key
  *                get out = 0 and lse = -inf.
  */
@@ -56,7 +59,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 2
+#define SAGE_ABI_VERSION 3
 
 enum sage_status {
   SAGE_OK = 0,
@@ -69,6 +72,7 @@ enum sage_status {
 enum sage_qk_kind { SAGE_QK_INT8 = 0, SAGE_QK_FP8 = 1 };
 enum sage_pv_kind { SAGE_PV_BF16 = 0, SAGE_PV_FP8 = 1 };
 enum sage_granularity { SAGE_GRAN_TOKEN = 0, SAGE_GRAN_BLOCK64 = 1 };
+enum sage_out_layout { SAGE_OUT_BHND = 0, SAGE_OUT_BNHD = 1 };
 
 /* Version of this ABI (SAGE_ABI_VERSION).  No reference counterpart. */
 int sage_abi_version(void);
@@ -109,8 +113,10 @@ int sage_quantize_qkv(const void* q, const void* k, const void* v,
 /* Bytes of device workspace sage_attn_fwd needs for B x H heads of N tokens
  * of dimension D: per-batch (min doc, max doc, #valid, #padding) summaries of
  * every 64-key tile and 32- and 128-row query block (written and used when
- * doc_ids is given).  No reference counterpart (the Triton launch needs no
- * workspace). */
+ * doc_ids is given), then the fp32 partial results of the key-tile pieces of
+ * the 128-row items that an unmasked launch splits (the items past the last
+ * whole round of 512 resident workgroups).  No reference counterpart (the
+ * Triton launch needs no workspace). */
 size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
 
 /* Fused attention forward over pre-quantized operands.
@@ -129,7 +135,11 @@ size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
  *   h             heads per batch (row z of q belongs to batch z / h).
  *   workspace     device memory of sage_attn_workspace_bytes(b, h, n, d)
  *                 bytes, 16-byte aligned.  Concurrent calls need separate
- *                 workspaces. */
+ *                 workspaces.
+ *   out_layout    SAGE_OUT_BHND (the reference op's output) or SAGE_OUT_BNHD
+ *                 (fuses JointAttention's out.transpose(1, 2).reshape(b, -1,
+ *                 H*D), transformer.py:471).  Values are bit-identical
+ *                 between the two layouts. */
 int sage_attn_fwd(const void* q_codes, const float* q_scale,
                   const void* k_codes, const float* k_scale,
                   const void* v_in, const float* v_scale,
@@ -139,7 +149,7 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale,
                   int64_t mask_nq, int64_t mask_nkv,
                   const int32_t* doc_ids,
                   void* workspace, size_t workspace_bytes,
-                  void* out, float* lse,
+                  void* out, int out_layout, float* lse,
                   hipStream_t stream);
 
 /* Debug/parity: int32 QK^T accumulators of int8 codes through the same MFMA

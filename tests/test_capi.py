@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), f"{name} declared in the header but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes prototype"
-    assert lib.sage_abi_version() == 2
+    assert lib.sage_abi_version() == 3
 
 
 def test_sizes_and_padding():
@@ -86,11 +86,11 @@ def test_quantize_rejects_bad_arguments(over, status, msg):
 
 def _attn_call(lib, **over):
     a = dict(qc=16, qs=32, kc=48, ks=64, vi=80, vs=96, b=1, h=2, n=300, d=128, qk=0, pv=1, gran=0,
-             mask=None, sz=0, nq=3, nkv=5, doc=None, ws=None, wsb=0, out=112, lse=128, stream=None)
+             mask=None, sz=0, nq=3, nkv=5, doc=None, ws=None, wsb=0, out=112, layout=0, lse=128, stream=None)
     a.update(over)
     return lib.sage_attn_fwd(a["qc"], a["qs"], a["kc"], a["ks"], a["vi"], a["vs"], a["b"], a["h"], a["n"], a["d"],
                              a["qk"], a["pv"], a["gran"], a["mask"], a["sz"], a["nq"], a["nkv"], a["doc"], a["ws"],
-                             a["wsb"], a["out"], a["lse"], a["stream"])
+                             a["wsb"], a["out"], a["layout"], a["lse"], a["stream"])
 
 
 @pytest.mark.parametrize("over,status,msg", [
@@ -104,6 +104,8 @@ def _attn_call(lib, **over):
     (dict(doc=256, ws=264, wsb=1 << 24), 2, "workspace must be 16-byte aligned"),
     (dict(out=None), 1, "null"),
     (dict(pv=1, vs=None), 1, "v_scale"),
+    (dict(layout=2), 1, "out_layout must be 0"),
+    (dict(layout=-1), 1, "out_layout must be 0"),
 ])
 def test_attn_rejects_bad_arguments(over, status, msg):
     from futudiffu_amd import _lib
@@ -144,6 +146,13 @@ def test_custom_op_schemas_and_fake_shapes():
         assert lse.shape == (6, 40) and lse.dtype == torch.float32
         out, lse = ops.sage_attn(q, q, q, 0.1)
         assert out.shape == (2, 3, 40, 128) and lse.shape == (6, 40)
+        # [B, N, H*D] output for the out-projection (transformer.py:471)
+        out, lse = ops.sage_attn_masked_merged_heads(q, q, q, m, 0.1)
+        assert out.shape == (2, 40, 384) and out.dtype == torch.bfloat16 and lse.shape == (6, 40)
+        out, lse = ops.sage_attn_ext(q, q, q, None, None, 0.1, "int8", "fp8", "token", True, "bnhd")
+        assert out.shape == (2, 40, 384) and lse.shape == (6, 40)
+        out, lse = ops.sage_attn_ext(q, q, q, None, None, 0.1, "int8", "fp8", "token", True)
+        assert out.shape == (2, 3, 40, 128)
 
 
 def test_layout_round_trip():
