@@ -426,7 +426,7 @@ def main():
         },
         "quantize": {
             "bound": "hbm",
-            "kernel": "k_sum_zero_kernel + quantize_kernel + k_quantize_kernel",
+            "kernel": "k_colsum_kernel + quantize_kernel",
             "achieved": round(q_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

@@ -74,6 +74,7 @@ int sage_quantize_qkv(const void* q, const void* k, const void* v, int64_t bh, i
     const size_t need = sage::quant_workspace_bytes(bh, n, d);
     if (!workspace || workspace_bytes < need)
       return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+    if (!aligned16(workspace)) return fail(SAGE_ERR_ALIGN, "workspace must be 16-byte aligned");
   }
   hipError_t e = sage::launch_quantize(
       qk_kind, pv_kind, granularity, smooth_k != 0, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),

@@ -10,13 +10,12 @@
 // loop; per-token scales depend only on the token, so quantizing once here
 // yields identical codes.
 //
-// quantize (one workgroup per 64-token block and head) issues all of its Q,
-// K and V loads up front, writes Q and V codes and adds the block's fp64 K
-// column sums into per-head sums (zeroed just before by k_sum_zero).
-// k_quantize then forms each head's mean and writes the K codes; it is the
-// only second read of K, which the mean makes unavoidable (every K code
-// depends on all N tokens).  Without smoothing, quantize writes the K codes
-// itself.
+// With smoothing, k_colsum first reads K once and writes fp64 column sums of
+// each 256-token chunk (no atomics, nothing to clear beforehand).  quantize
+// (one workgroup per 64-token block and head) then issues all of its Q, K and
+// V loads up front, adds the chunk sums of its head in a fixed order to form
+// the mean, and writes the Q, K and V codes.  The mean makes the second read
+// of K unavoidable: every K code depends on all N tokens.
 #include "sage_common.h"
 #include "sage_launch.h"
 
@@ -50,6 +49,8 @@ __device__ __forceinline__ float rows_max(float a) {
   const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
   return fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
 }
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t word_of(uint4 w, int i) {
   return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
@@ -112,23 +113,81 @@ __device__ __forceinline__ void row_amax(const float (&x)[PASSES][8], float (&am
   }
 }
 
-// Pass 2: one workgroup per (64-token block, bh).
+// Tokens per K column-sum chunk.
+constexpr int kSumTokens = 256;
+
+__host__ __device__ inline int64_t k_sum_chunks(int64_t n) { return (n + kSumTokens - 1) / kSumTokens; }
+
+// Smoothing pass 1: fp64 column sums of K over each 256-token chunk of each
+// head, part[bh][chunk][d].  One workgroup per (chunk, bh); lane (rr, c8)
+// holds channels [8*c8, +8) of tokens rr + RPP*ps.  Every sum is formed in a
+// fixed order, so the result does not depend on scheduling.
+template <int D>
+__global__ void __launch_bounds__(256) k_colsum_kernel(const uint16_t* __restrict__ k, int64_t n,
+                                                       double* __restrict__ part) {
+  constexpr int LPR = D / 8;
+  constexpr int RPP = 256 / LPR;
+  constexpr int PASSES = kSumTokens / RPP;
+  __shared__ double ksw[4][D];
+  const int bh = blockIdx.y, ch = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
+  const int c8 = tid % LPR, rr = tid / LPR;
+  const int64_t tok0 = (int64_t)ch * kSumTokens;
+  const uint16_t* kb = k + (int64_t)bh * n * D + c8 * 8;
+  uint4 w[PASSES];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int64_t tok = min(tok0 + rr + ps * RPP, n - 1);  // clamped in bounds, masked below
+    w[ps] = *reinterpret_cast<const uint4*>(kb + tok * D);
+  }
+  double cs[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) cs[e] = 0.0;
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    float x[8];
+    unpack8(w[ps], x);
+    const bool keep = tok0 + rr + ps * RPP < n;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cs[e] += keep ? (double)x[e] : 0.0;
+  }
+  // token rows of the wave (lanes c8 + LPR*m), then the 4 waves
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) cs[e] += __shfl_xor(cs[e], off);
+  if ((tid & 63) < LPR) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ksw[wave][c8 * 8 + e] = cs[e];
+  }
+  __syncthreads();
+  if (tid < D)
+    part[((int64_t)bh * gridDim.x + ch) * D + tid] = (ksw[0][tid] + ksw[1][tid]) + (ksw[2][tid] + ksw[3][tid]);
+}
+
+// One workgroup per (64-token block, bh).
 //   Q, K: lane (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps.
 //   V:    lane (g, c8) holds channels [8*c8, +8) of the 4 consecutive tokens
 //         4g..4g+3, so the 4 codes of a channel form one 32-bit fragment word.
+// With smoothing, the head's mean is the sum of its chunk sums (fixed order)
+// / N in fp64, rounded to fp32 then bf16 (the reference's bf16 mean), and K
+// rows are smoothed as bf16(k - mean).
 template <int D, int QK, int PV, int GRAN, bool SMOOTH>
 __global__ void __launch_bounds__(256) quantize_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    int64_t n, int64_t np, float fold, double* __restrict__ ksum,
+    int64_t n, int64_t np, float fold, const double* __restrict__ ksum_part,
     uint8_t* __restrict__ qc, float* __restrict__ qs, uint8_t* __restrict__ kc, float* __restrict__ ks,
-    uint8_t* __restrict__ vout, float* __restrict__ vs) {
+    uint8_t* __restrict__ vout, float* __restrict__ vs, uint16_t* __restrict__ kmean) {
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   constexpr int PASSES = 64 / RPP;
   constexpr int VTHREADS = 16 * LPR;  // 16 groups of 4 tokens
   __shared__ unsigned int blk_amax[2];
   __shared__ __attribute__((aligned(16))) float vmax[4][D];
-  __shared__ double ksw[SMOOTH ? 4 : 1][D];
+  // smoothing: the TPC threads of a column each sum every TPC-th chunk sum
+  constexpr int TPC = 256 / D;
+  constexpr int kMeanLoads = 12;  // chunk sums in flight per thread
+  __shared__ double msum[SMOOTH ? TPC : 1][D];
+  __shared__ float mu[SMOOTH ? D : 1];
   // V operand image of this 64-token block in fragment order; written to
   // global as contiguous 16-byte chunks
   __shared__ __attribute__((aligned(16))) uint8_t vimg[(PV == kPV_FP8 ? 1 : 2) * 64 * D];
@@ -141,6 +200,16 @@ __global__ void __launch_bounds__(256) quantize_kernel(
 
   if (tid < 2) blk_amax[tid] = 0u;
   __syncthreads();
+
+  // ---- smoothing: this thread's chunk sums, loaded before the block's data ----
+  // Thread (j = tid / D, column tid % D) adds chunks j, j + TPC, ... in order.
+  const int64_t nch = SMOOTH ? k_sum_chunks(n) : 0;
+  const double* pp = ksum_part + ((int64_t)bh * nch + tid / D) * D + tid % D;
+  double mt[SMOOTH ? kMeanLoads : 1];
+  if constexpr (SMOOTH) {
+#pragma unroll
+    for (int i = 0; i < kMeanLoads; ++i) mt[i] = tid / D + TPC * i < nch ? pp[(int64_t)TPC * i * D] : 0.0;
+  }
 
   // ---- issue every load of the block up front ------------------------------
   // Token indices are clamped to N-1 so every load is in bounds and issued
@@ -169,6 +238,13 @@ __global__ void __launch_bounds__(256) quantize_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (tid >= VTHREADS || tok0 + 4 * g + i >= n) vw[i] = zero4;
+  if constexpr (SMOOTH) {
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < kMeanLoads; ++i) s += mt[i];
+    for (int64_t c = tid / D + TPC * kMeanLoads; c < nch; c += TPC) s += pp[(c - tid / D) * D];  // long heads
+    msum[tid / D][tid % D] = s;  // combined after the V section's barrier
+  }
   // ---- Q -----------------------------------------------------------------------
   {
     float x[PASSES][8], amax[PASSES];
@@ -180,11 +256,18 @@ __global__ void __launch_bounds__(256) quantize_kernel(
 
   // ---- V -------------------------------------------------------------------------
   if (PV == kPV_FP8) {
-    float x[4][8], cm[8];
+    // channel maxima of |v| over the 4 tokens, on the bf16 bit patterns: for
+    // non-NaN values the magnitude bits order like the magnitudes, and the
+    // 32 unpacked floats need not stay live across the barrier below
+    float cm[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) unpack8(vw[i], x[i]);
+    for (int w4 = 0; w4 < 4; ++w4) {
+      u16x2 m = __builtin_bit_cast(u16x2, word_of(vw[0], w4) & 0x7fff7fffu);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) cm[e] = fmaxf(fmaxf(fabsf(x[0][e]), fabsf(x[1][e])), fmaxf(fabsf(x[2][e]), fabsf(x[3][e])));
+      for (int i = 1; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, word_of(vw[i], w4) & 0x7fff7fffu));
+      cm[2 * w4] = __uint_as_float((uint32_t)m.x << 16);
+      cm[2 * w4 + 1] = __uint_as_float((uint32_t)m.y << 16);
+    }
     // across the token groups of this wave (lanes c8 + LPR*m), then across waves
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -234,7 +317,13 @@ __global__ void __launch_bounds__(256) quantize_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int d = c8 * 8 + e, j = d >> 5, r = d & 31;
-        const uint32_t word = pack_fp8x4(x[0][e] * inv[e], x[1][e] * inv[e], x[2][e] * inv[e], x[3][e] * inv[e]);
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w = word_of(vw[i], e >> 1);
+          x[i] = __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+        }
+        const uint32_t word = pack_fp8x4(x[0] * inv[e], x[1] * inv[e], x[2] * inv[e], x[3] * inv[e]);
         *reinterpret_cast<uint32_t*>(vimg + (((j * 2 + b) * 64 + 32 * hh + r) * 16) + 4 * jj) = word;
       }
     }
@@ -256,6 +345,16 @@ __global__ void __launch_bounds__(256) quantize_kernel(
     }
   }
   __syncthreads();
+  if constexpr (SMOOTH) {
+    if (tid < D) {
+      double s = msum[0][tid];
+#pragma unroll
+      for (int j = 1; j < TPC; ++j) s += msum[j][tid];
+      const uint16_t m16 = f32_to_bf16_rne((float)(s / (double)n));
+      mu[tid] = bf16_to_f32(m16);
+      if (blk == 0) kmean[(int64_t)bh * D + tid] = m16;
+    }
+  }
   {
     constexpr int VBYTES = (PV == kPV_FP8 ? 1 : 2) * 64 * D;
     uint8_t* vo = vout + (PV == kPV_FP8 ? 1 : 2) * (co + tok0 * D);
@@ -263,89 +362,24 @@ __global__ void __launch_bounds__(256) quantize_kernel(
     for (int i = tid; i < VBYTES / 16; i += 256)
       reinterpret_cast<uint4*>(vo)[i] = reinterpret_cast<const uint4*>(vimg)[i];
   }
+  if constexpr (SMOOTH) __syncthreads();  // mu
 
-  // ---- K: codes right away without smoothing; with smoothing, this block's
-  // fp64 column sums (exact) for the mean, and k_quantize_kernel does the codes
-  if constexpr (!SMOOTH) {
+  // ---- K ---------------------------------------------------------------------
+  {
     float x[PASSES][8], amax[PASSES];
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) unpack8(kw[ps], x[ps]);
+    for (int ps = 0; ps < PASSES; ++ps) {
+      unpack8(kw[ps], x[ps]);
+      if constexpr (SMOOTH) {
+        // rows past N were loaded as zeros; keep them zero after the shift
+        const float keep = tok0 + rr + ps * RPP < n ? 1.0f : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[ps][e] = bf16_to_f32(f32_to_bf16_rne(x[ps][e] - mu[c8 * 8 + e])) * keep;
+      }
+    }
     row_amax<D, GRAN, PASSES>(x, amax, &blk_amax[1]);
     store_rows<D, QK, GRAN, PASSES>(x, amax, tok0, rr, c8, 1.0f, kc + co, ks + sco, tid);
-  } else {
-    double cs[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) cs[e] = 0.0;
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      float x[8];
-      unpack8(kw[ps], x);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) cs[e] += (double)x[e];
-    }
-    // token rows of the wave (lanes c8 + LPR*m), then the 4 waves
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int off = LPR; off < 64; off <<= 1) cs[e] += __shfl_xor(cs[e], off);
-    if ((tid & 63) < LPR) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ksw[wave][c8 * 8 + e] = cs[e];
-    }
-    __syncthreads();
-    // fp64 sums of bf16 values are exact, so the order of these additions
-    // does not change the result
-    if (tid < D) unsafeAtomicAdd(&ksum[(int64_t)bh * D + tid], (ksw[0][tid] + ksw[1][tid]) + (ksw[2][tid] + ksw[3][tid]));
   }
-}
-
-// Zero the per-head K column sums before quantize accumulates into them.
-__global__ void __launch_bounds__(256) k_sum_zero_kernel(double* __restrict__ ksum, int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < count) ksum[i] = 0.0;
-}
-
-// Pass 2 (smoothing on): K codes, one workgroup per (64-token block, bh).
-// The head's mean is its column sum / N in fp64, rounded to fp32 then bf16
-// (the reference's bf16 mean); K rows are smoothed as bf16(k - mean).
-template <int D, int QK, int GRAN>
-__global__ void __launch_bounds__(256) k_quantize_kernel(const uint16_t* __restrict__ k, int64_t n, int64_t np,
-                                                         const double* __restrict__ ksum, uint8_t* __restrict__ kc,
-                                                         float* __restrict__ ks, uint16_t* __restrict__ kmean) {
-  constexpr int LPR = D / 8;
-  constexpr int RPP = 256 / LPR;
-  constexpr int PASSES = 64 / RPP;
-  __shared__ float mu[D];
-  __shared__ unsigned int blk_amax;
-  const int bh = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
-  const int c8 = tid % LPR, rr = tid / LPR;
-  const int64_t tok0 = (int64_t)blk * 64;
-  const int64_t so = (int64_t)bh * n * D;
-  const int64_t co = (int64_t)bh * np * D;
-  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
-  uint4 w[PASSES];
-#pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) {
-    const int64_t tok = min(tok0 + rr + ps * RPP, n - 1);  // clamped, masked below
-    w[ps] = *reinterpret_cast<const uint4*>(k + so + tok * D + c8 * 8);
-  }
-  if (tid == 0) blk_amax = 0u;
-  if (tid < D) {
-    const uint16_t m16 = f32_to_bf16_rne((float)(ksum[(int64_t)bh * D + tid] / (double)n));
-    mu[tid] = bf16_to_f32(m16);
-    if (blk == 0) kmean[(int64_t)bh * D + tid] = m16;
-  }
-  __syncthreads();
-  float x[PASSES][8], amax[PASSES];
-#pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) {
-    unpack8(w[ps], x[ps]);
-    const float keep = tok0 + rr + ps * RPP < n ? 1.0f : 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[ps][e] = bf16_to_f32(f32_to_bf16_rne(x[ps][e] - mu[c8 * 8 + e])) * keep;
-  }
-  row_amax<D, GRAN, PASSES>(x, amax, &blk_amax);
-  store_rows<D, QK, GRAN, PASSES>(x, amax, tok0, rr, c8, 1.0f, kc + co, ks + sco, tid);
 }
 
 template <int D, int QK, int PV, int GRAN, bool SMOOTH>
@@ -355,14 +389,11 @@ hipError_t launch_quantize_t(const uint16_t* q, const uint16_t* k, const uint16_
   const int64_t np = padded_len(n);
   const int nblk = (int)(np / 64);
   if (SMOOTH) {
-    hipLaunchKernelGGL(k_sum_zero_kernel, dim3((unsigned)((bh * D + 255) / 256)), dim3(256), 0, st, ws, bh * D);
+    hipLaunchKernelGGL(k_colsum_kernel<D>, dim3((unsigned)k_sum_chunks(n), (unsigned)bh), dim3(256), 0, st, k, n,
+                       ws);
   }
   hipLaunchKernelGGL((quantize_kernel<D, QK, PV, GRAN, SMOOTH>), dim3((unsigned)nblk, (unsigned)bh), dim3(256), 0,
-                     st, q, k, v, n, np, fold, ws, qc, qs, kc, ks, vout, vs);
-  if (SMOOTH) {
-    hipLaunchKernelGGL((k_quantize_kernel<D, QK, GRAN>), dim3((unsigned)nblk, (unsigned)bh), dim3(256), 0, st, k, n,
-                       np, ws, kc, ks, kmean);
-  }
+                     st, q, k, v, n, np, fold, ws, qc, qs, kc, ks, vout, vs, kmean);
   return hipGetLastError();
 }
 
@@ -404,10 +435,9 @@ hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t
   return hipErrorInvalidValue;
 }
 
-// fp64 column sums of K per head, [bh][d].
+// fp64 column sums of K per head and 256-token chunk, [bh][ceil(n/256)][d].
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d) {
-  (void)n;
-  return (size_t)(bh * d) * sizeof(double);
+  return (size_t)(bh * k_sum_chunks(n) * d) * sizeof(double);
 }
 
 }  // namespace sage

@@ -43,7 +43,10 @@ def test_sizes_and_padding():
     from futudiffu_amd import _lib
     lib = _lib.load()
     assert [lib.sage_padded_len(n) for n in (1, 128, 129, 4416)] == [128, 128, 256, 4480]
-    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 128 * 8
+    # fp64 K column sums per head and 256-token chunk
+    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 18 * 128 * 8
+    assert lib.sage_quant_workspace_bytes(2, 256, 64) == 2 * 1 * 64 * 8
+    assert lib.sage_quant_workspace_bytes(1, 257, 64) == 2 * 64 * 8
     # per-batch summaries of every 64-key tile and 32- and 128-row query block,
     # then (256-byte aligned) fp32 slots of 128 x D + 512 floats for the pieces
     # of the split tail: 26 items x 8 pieces at the 1x30x4416x128 headline shape
@@ -75,6 +78,7 @@ def _quant_call(lib, **over):
     (dict(k=33), 2, "aligned"),
     (dict(km=None), 1, "k_mean"),
     (dict(wsb=8), 3, "workspace"),
+    (dict(ws=184), 2, "workspace must be 16-byte aligned"),
     (dict(bh=70000), 1, "grid"),
 ])
 def test_quantize_rejects_bad_arguments(over, status, msg):
