@@ -58,41 +58,59 @@ __device__ __forceinline__ int classify(int4 qsum, int4 ksum) {
 }
 
 // Per-batch token summaries: kv tiles of 64, query blocks of 32 and of 128.
-__global__ void doc_summary_kernel(const int32_t* __restrict__ doc, int64_t n, int64_t np, int nb, int nt,
-                                   int4* __restrict__ kv_sum, int4* __restrict__ q_sum, int4* __restrict__ q_sum128) {
+// One wave per summary (grid-stride over summaries): lane l reads tokens
+// t0 + l and t0 + 64 + l, then wave-wide min / max / sums.
+__global__ void __launch_bounds__(256) doc_summary_kernel(const int32_t* __restrict__ doc, int64_t n, int64_t np,
+                                                          int nb, int nt, int4* __restrict__ kv_sum,
+                                                          int4* __restrict__ q_sum, int4* __restrict__ q_sum128) {
   const int64_t nq32 = np / 32, nq128 = np / 128;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int64_t per_b = nt + nq32 + nq128;
-  if (idx >= (int64_t)nb * per_b) return;
-  const int b = (int)(idx / per_b);
-  const int64_t w = idx % per_b;
-  int64_t t0, len;
-  int4* dst;
-  if (w < nt) {
-    t0 = w * 64;
-    len = 64;
-    dst = kv_sum + (int64_t)b * nt + w;
-  } else if (w < nt + nq32) {
-    t0 = (w - nt) * 32;
-    len = 32;
-    dst = q_sum + (int64_t)b * nq32 + (w - nt);
-  } else {
-    t0 = (w - nt - nq32) * 128;
-    len = 128;
-    dst = q_sum128 + (int64_t)b * nq128 + (w - nt - nq32);
-  }
-  int mn = 0x7fffffff, mx = -0x7fffffff, nv = 0, ni = 0;
-  for (int64_t i = t0; i < t0 + len && i < n; ++i) {
-    const int dd = doc[(int64_t)b * n + i];
-    if (dd >= 0) {
-      mn = min(mn, dd);
-      mx = max(mx, dd);
-      ++nv;
+  const int64_t total = (int64_t)nb * per_b;
+  const int64_t stride = (int64_t)gridDim.x * (blockDim.x >> 6);
+  // idx is wave-uniform: every lane of a wave runs the same iterations
+  for (int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; idx < total; idx += stride) {
+    const int b = (int)(idx / per_b);
+    const int64_t w = idx % per_b;
+    int64_t t0, len;
+    int4* dst;
+    if (w < nt) {
+      t0 = w * 64;
+      len = 64;
+      dst = kv_sum + (int64_t)b * nt + w;
+    } else if (w < nt + nq32) {
+      t0 = (w - nt) * 32;
+      len = 32;
+      dst = q_sum + (int64_t)b * nq32 + (w - nt);
     } else {
-      ++ni;
+      t0 = (w - nt - nq32) * 128;
+      len = 128;
+      dst = q_sum128 + (int64_t)b * nq128 + (w - nt - nq32);
     }
+    int mn = 0x7fffffff, mx = -0x7fffffff, nv = 0, ni = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int64_t i = t0 + 64 * s + lane;
+      if (64 * s + lane < len && i < n) {
+        const int dd = doc[(int64_t)b * n + i];
+        if (dd >= 0) {
+          mn = min(mn, dd);
+          mx = max(mx, dd);
+          ++nv;
+        } else {
+          ++ni;
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      mn = min(mn, __shfl_xor(mn, off));
+      mx = max(mx, __shfl_xor(mx, off));
+      nv += __shfl_xor(nv, off);
+      ni += __shfl_xor(ni, off);
+    }
+    if (lane == 0) *dst = make_int4(mn, mx, nv, ni);
   }
-  *dst = make_int4(mn, mx, nv, ni);
 }
 
 // LDS stage layout (bytes): K codes, V operand, per-key K scales, per-key
@@ -794,8 +812,9 @@ hipError_t launch_attn_d(int qk, int pv, int gran, int mask, const AttnParams& p
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb,
                        hipStream_t st) {
   if (mask & 2) {
-    const int64_t total = (int64_t)nb * (p.nt + p.np / 32 + p.np / 128);
-    hipLaunchKernelGGL(doc_summary_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p.doc, p.n,
+    const int64_t total = (int64_t)nb * (p.nt + p.np / 32 + p.np / 128);  // summaries, one wave each
+    const int64_t blocks = (total + 3) / 4 < 8192 ? (total + 3) / 4 : 8192;
+    hipLaunchKernelGGL(doc_summary_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p.doc, p.n,
                        p.np, nb, p.nt, const_cast<int4*>(p.kv_sum), const_cast<int4*>(p.q_sum),
                        const_cast<int4*>(p.q_sum128));
   }
