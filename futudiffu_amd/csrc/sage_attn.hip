@@ -32,7 +32,8 @@
 // fp8 P follows the reference per (row, 64-key block) scaling
 // (sage_kernels.py:1137-1141): with bm the block's row max, the code argument
 // is e = 2^(s - bm) * 448 (= p * 448 / max(p)), and the block's PV product is
-// dequantized by 2^(bm - m_ref) / 448 per row and the V scale per channel.
+// dequantized by 2^(bm - m_ref) / 448 per row and the V scale per channel
+// (the rank-1 factor matrix comes from a small fp32 MFMA).
 // bf16 P is 2^(s - m_ref) rounded to bf16; bf16 rounding is relative, so this
 // matches the reference's bf16(2^(s - m)) up to exp2 rounding.
 #include <algorithm>
@@ -43,6 +44,7 @@
 namespace sage {
 
 constexpr float kLog2Fp8Max = 8.807354922057604f;  // log2(448)
+typedef float f32x32 __attribute__((ext_vector_type(32)));
 
 // Tile class for a block of queries against one key tile:
 // 0 = nothing visible, 1 = everything visible, 2 = per-token mask needed.
@@ -348,26 +350,27 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
         pa[4 * b + j] = (int)pack_fp8x4(e4[0], e4[1], e4[2], e4[3]);
       }
     l_acc = fmaf(rsc, (es[0] + es[1]) + (es[2] + es[3]), l_acc);
-    float rrow[16];
-    rows_of(xrow, rsc, h, r, rrow);
     const i32x4* vl = reinterpret_cast<const i32x4*>(sb + St::offV);
     const float* vdl = reinterpret_cast<const float*>(sb + St::offVd);
-    f32x16 part[2];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
+    auto pv = [&](int c) {
       const i32x4 b0 = vl[(c * 2 + 0) * 64 + lane], b1 = vl[(c * 2 + 1) * 64 + lane];
       const i32x8 bv = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-      part[c & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(pa, bv, f32x16{0}, 0, 0, 0, 0, 0, 0);
-      if (c >= 1) {
-        const float vd = vdl[32 * (c - 1) + r];
+      return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(pa, bv, f32x16{0}, 0, 0, 0, 0, 0, 0);
+    };
+    // The per-element factors rsc[row] * vd[channel] are rank-1 products, made
+    // on the matrix cores already in the O layout: v_mfma_f32_32x32x1_2b_f32
+    // forms two 32x32 outer products, block b from the lanes h = b, with A =
+    // rsc of query r (lane-local in the S^T layout) and B = the V scale of
+    // channel 32(c2 + b) + r.  Each product is one correctly rounded fp32
+    // multiply, as on the vector ALU, and no lane exchange is needed.
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[c - 1][e] = fmaf(part[(c - 1) & 1][e], rrow[e] * vd, o[c - 1][e]);
-      }
-    }
-    {
-      const float vd = vdl[32 * (NC - 1) + r];
+    for (int c2 = 0; c2 < NC; c2 += 2) {
+      const f32x32 rv = __builtin_amdgcn_mfma_f32_32x32x1f32(rsc, vdl[32 * (c2 + h) + r], f32x32{0}, 0, 0, 0);
+      const f32x16 p0 = pv(c2), p1 = pv(c2 + 1);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[NC - 1][e] = fmaf(part[(NC - 1) & 1][e], rrow[e] * vd, o[NC - 1][e]);
+      for (int e = 0; e < 16; ++e) o[c2][e] = fmaf(p0[e], rv[e], o[c2][e]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[c2 + 1][e] = fmaf(p1[e], rv[16 + e], o[c2 + 1][e]);
     }
   } else {
     // bf16 P = 2^(s - m_ref) <= 2^kTau, accumulated straight into O
