@@ -335,7 +335,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the forward shards by head with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the forward shards by head with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

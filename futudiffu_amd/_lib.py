@@ -30,6 +30,8 @@ SIGNATURES = {
         _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_int,
         _P, _I64, _I64, _I64, _P, _P, _c.c_size_t, _P, _c.c_int, _P, _P]),
     "sage_qk_int32": (_c.c_int, [_P, _P, _I64, _I64, _I64, _P, _P]),
+    "sage_build_tile_mask": (_c.c_int, [_P, _I64, _I64, _c.c_int32, _P, _P]),
+    "sage_doc_ids_from_cu_seqlens": (_c.c_int, [_P, _I64, _I64, _I64, _P, _P]),
 }
 
 _lock = threading.Lock()
@@ -50,7 +52,7 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
-            if lib.sage_abi_version() != 3:
+            if lib.sage_abi_version() != 4:
                 raise RuntimeError("libsage_mi355x.so ABI version mismatch")
             _lib = lib
         return _lib

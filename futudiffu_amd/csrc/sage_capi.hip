@@ -168,6 +168,26 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
   return launch_status(e, "sage_attn_fwd");
 }
 
+int sage_build_tile_mask(const int32_t* doc_ids, int64_t b, int64_t n, int32_t pad_fill, uint8_t* mask,
+                         hipStream_t stream) {
+  if (b <= 0 || n <= 0) return fail(SAGE_ERR_ARG, "b=%lld and n=%lld must be positive", (long long)b, (long long)n);
+  if (b > 65535) return fail(SAGE_ERR_ARG, "b=%lld exceeds the grid limit 65535", (long long)b);
+  if (n > (int64_t)1 << 24) return fail(SAGE_ERR_ARG, "n=%lld exceeds 2^24", (long long)n);
+  if (!doc_ids || !mask) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  return launch_status(sage::launch_tile_mask(doc_ids, b, n, pad_fill, mask, stream), "sage_build_tile_mask");
+}
+
+int sage_doc_ids_from_cu_seqlens(const int32_t* cu_seqlens, int64_t b, int64_t n_segments, int64_t n,
+                                 int32_t* doc_ids, hipStream_t stream) {
+  if (b <= 0 || n <= 0) return fail(SAGE_ERR_ARG, "b=%lld and n=%lld must be positive", (long long)b, (long long)n);
+  if (n_segments < 0) return fail(SAGE_ERR_ARG, "n_segments=%lld must not be negative", (long long)n_segments);
+  if (b > 65535) return fail(SAGE_ERR_ARG, "b=%lld exceeds the grid limit 65535", (long long)b);
+  if (n > (int64_t)1 << 24) return fail(SAGE_ERR_ARG, "n=%lld exceeds 2^24", (long long)n);
+  if (!cu_seqlens || !doc_ids) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  return launch_status(sage::launch_doc_from_cu(cu_seqlens, b, n_segments, n, doc_ids, stream),
+                       "sage_doc_ids_from_cu_seqlens");
+}
+
 int sage_qk_int32(const void* q_codes, const void* k_codes, int64_t bh, int64_t n, int64_t d, int32_t* s_out,
                   hipStream_t stream) {
   int st = check_common(bh, n, d, SAGE_QK_INT8, SAGE_PV_BF16, SAGE_GRAN_TOKEN);

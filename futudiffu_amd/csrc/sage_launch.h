@@ -93,5 +93,9 @@ AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d);
 size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
 hipError_t launch_qk_int32(const uint8_t* qc, const uint8_t* kc, int64_t bh, int64_t n, int64_t d, int32_t* s,
                            hipStream_t st);
+hipError_t launch_tile_mask(const int32_t* doc, int64_t nb, int64_t n, int32_t pad_fill, uint8_t* mask,
+                            hipStream_t st);
+hipError_t launch_doc_from_cu(const int32_t* cu, int64_t nb, int64_t nseg, int64_t n, int32_t* doc,
+                              hipStream_t st);
 
 }  // namespace sage

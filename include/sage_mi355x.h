@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 3
+#define SAGE_ABI_VERSION 4
 
 enum sage_status {
   SAGE_OK = 0,
@@ -153,6 +153,34 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale,
                   void* workspace, size_t workspace_bytes,
                   void* out, int out_layout, float* lse,
                   hipStream_t stream);
+
+/* Reference tile mask from device per-token document ids.
+ * Replaces the host construction of build_block_mask /
+ * build_block_mask_from_packing_info (src_ii/block_mask.py:35-129): Q tile i
+ * (128 tokens) and KV tile j (64 tokens) take the id of their first token
+ * (tile starts clamped to n-1, :84-93), and mask[z][i][j] = 1 iff the ids
+ * are equal (:96-97).  Ids below zero (padding, as _pad_plan_to_fixed_len
+ * writes them, forward_packed.py:56-62) count as pad_fill; 0 reproduces the
+ * reference, where tokens past the last segment belong to document 0
+ * (block_mask.py:75-79).
+ *   doc_ids   int32 [b, n] device memory.
+ *   mask      uint8 [b, ceil(n/128), ceil(n/64)] (b = 1: the 2D reference mask). */
+int sage_build_tile_mask(const int32_t* doc_ids, int64_t b, int64_t n,
+                         int32_t pad_fill, uint8_t* mask, hipStream_t stream);
+
+/* Exact per-token document ids from varlen segment offsets, for the doc_ids
+ * argument of sage_attn_fwd.  No reference counterpart: it replaces the host
+ * list that build_packed_sequence fills per segment
+ * (src_ii/transformer.py:137-153) with the cu_seqlens form.
+ *   cu_seqlens  int32 [b, n_segments + 1] device memory, nondecreasing per
+ *               batch row; segment s covers tokens [cu[s], cu[s+1]).
+ *   doc_ids     int32 [b, n]: the segment index, or -1 for tokens outside
+ *               every segment (padding).
+ * Offsets that are not nondecreasing give unspecified ids, never an
+ * out-of-bounds access. */
+int sage_doc_ids_from_cu_seqlens(const int32_t* cu_seqlens, int64_t b,
+                                 int64_t n_segments, int64_t n,
+                                 int32_t* doc_ids, hipStream_t stream);
 
 /* Debug/parity: int32 QK^T accumulators of int8 codes through the same MFMA
  * fragments as sage_attn_fwd, s_out int32 [BH, Np, Np] (row = query).

@@ -11,8 +11,9 @@ forward as implemented by the Triton kernels of sqcu/futudiffu
 (``src/futudiffu/sage_attention.py``).  Each function cites the reference lines
 it follows.  Every function here is pinned by a check in
 ``tests/test_oracle.py`` (closed forms, invariants, brute force on tiny
-inputs) and by the committed fixtures in ``tests/golden/``; the reference has
-no golden vectors or known-answer tests for this path.
+inputs; the packed-plan mask helpers in ``tests/test_masks.py``) and by the
+committed fixtures in ``tests/golden/``; the reference has no golden vectors
+or known-answer tests for this path.
 
 Conventions (all follow the reference):
   * q, k, v are bf16 ``[B, H, N, D]``; internal math flattens to ``[BH, N, D]``.
@@ -26,7 +27,7 @@ Conventions (all follow the reference):
       fp8 : ``inv = 448 / max(amax, 1e-12)``, ``code = e4m3fn_rne(x * inv)``,
             ``scale = amax / 448`` (sage_kernels.py:250-258, :272-280).
       The Q scale has ``sm_scale*log2(e)`` folded in (:1422, :258).
-  * "block64" granularity (one scale per 64 tokens) is the BASELINE config's
+  * "block64" granularity (one scale per 64 tokens) is the CPU plumbing case's
     variant; it applies the same formulas with amax over a 64-token block.
 
 Deviation that is a definition, not an approximation:
@@ -204,6 +205,48 @@ def build_block_mask(segment_lengths: list[int], total_len: int | None = None) -
     kd = [doc[min(j * BLOCK_N, total_len - 1)] for j in range(nk)]
     return torch.tensor([[1 if qd[i] == kd[j] else 0 for j in range(nk)] for i in range(nq)],
                         dtype=torch.uint8)
+
+
+def packed_document_ids(segment_lengths: list[int], target_len: int | None = None) -> list[int]:
+    """Per-token document ids of a packed plan, as ``build_packed_sequence``
+    writes them (segment i -> id i, transformer.py:137-153) and
+    ``_pad_plan_to_fixed_len`` pads them (-1 up to ``target_len``,
+    forward_packed.py:56-62; longer plans raise ValueError, :47-51)."""
+    doc = [i for i, s in enumerate(segment_lengths) for _ in range(s)]
+    if target_len is not None:
+        if len(doc) > target_len:
+            raise ValueError(f"packed length {len(doc)} exceeds {target_len}")
+        doc += [-1] * (target_len - len(doc))
+    return doc
+
+
+def tile_mask_from_doc(doc: list[int], pad_fill: int = 0) -> torch.Tensor:
+    """The reference tile rule (block_mask.py:84-97) evaluated on per-token
+    document ids: tile starts clamped to ``N-1``, mask = equality of the first
+    tokens' ids.  Ids below zero (padding) count as ``pad_fill``: with 0 this is
+    the reference's view of tokens past the last segment (block_mask.py:75-79)."""
+    n = len(doc)
+    d = [pad_fill if x < 0 else x for x in doc]
+    nq = (n + BLOCK_M - 1) // BLOCK_M
+    nk = (n + BLOCK_N - 1) // BLOCK_N
+    qd = [d[min(i * BLOCK_M, n - 1)] for i in range(nq)]
+    kd = [d[min(j * BLOCK_N, n - 1)] for j in range(nk)]
+    return torch.tensor([[1 if qd[i] == kd[j] else 0 for j in range(nk)] for i in range(nq)],
+                        dtype=torch.uint8)
+
+
+def doc_ids_from_cu_seqlens(cu: list[int], n: int) -> list[int]:
+    """Exact per-token ids from segment offsets ``cu`` (segment s covers tokens
+    ``[cu[s], cu[s+1])``, the varlen form of build_packed_sequence's layout,
+    transformer.py:137-153); tokens outside every segment are padding (-1).
+    ``cu`` is nondecreasing, so the segments are disjoint."""
+    doc = [-1] * n
+    for t in range(n):
+        for s in range(len(cu) - 1):
+            if cu[s] <= t < cu[s + 1]:
+                doc[t] = s
+                break
+    return doc
 
 
 def doc_visibility(doc_ids: torch.Tensor) -> torch.Tensor:
@@ -404,7 +447,7 @@ def sdpa_fp64(q, k, v, sm_scale=None, visible=None):
 
 
 def make_inputs(b, h, n, d, seed=0, k_offset_std=2.0):
-    """Seeded inputs of the BASELINE distribution: q, k, v ~ N(0,1) bf16 and a
+    """Seeded inputs of the benchmark distribution: q, k, v ~ N(0,1) bf16 and a
     per-(b, h, channel) K offset ~ N(0, std=k_offset_std) added before the bf16 cast."""
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(b, h, n, d, generator=g)
