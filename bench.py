@@ -84,6 +84,11 @@ CASES = {
     # [B, N, H*D] input, timed against [B, H, N, D] + the caller's transpose copy
     "dit1280x832_int8fp8_outproj": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="fp8", gran="token",
                                         out="bnhd"),
+    # the 1280x832 shape from the QKV projection output: the q/k/v producer
+    # (RMSNorm + RoPE) inside the quantization, timed against the producer
+    # writing bf16 q, k, v followed by the quantization
+    "dit1280x832_int8fp8_from_qkv": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="fp8", gran="token",
+                                         producer=True),
 }
 PEAK_MIXED_TFLOPS = 2.0 / (1.0 / PEAK_8BIT_TFLOPS + 1.0 / PEAK_BF16_TFLOPS)  # fp8 QK + bf16 PV
 
@@ -279,11 +284,27 @@ def all_configs(args):
         docd = None if doc is None else doc.to(dev)
         sm = 1.0 / math.sqrt(D)
         layout = c.get("out", "bhnd")
+        if c.get("producer"):
+            g = torch.Generator(device="cpu").manual_seed(1)
+            qkv = torch.randn(B, N, 3 * H * D, generator=g).bfloat16().to(dev)
+            nw = (1.0 + 0.1 * torch.randn(2, D, generator=g)).to(dev)
+            ang = torch.rand(B, N, 1, D // 2, generator=g) * 6.283
+            cs, sn = torch.cos(ang), torch.sin(ang)
+            freqs = torch.stack([torch.stack([cs, -sn], -1), torch.stack([sn, cs], -1)], -2).to(dev)
 
-        def step(ev=None, out_layout=layout, merge_heads=False):
+        def quantize(fused=True):
+            if not c.get("producer"):
+                return SA.quantize_qkv(qd, kd, vd, sm, qk=c["qk"], pv=c["pv"], granularity=c["gran"])
+            if fused:
+                return SA.quantize_from_qkv(qkv, nw[0], nw[1], freqs, H, D, 1e-5, sm, qk=c["qk"], pv=c["pv"],
+                                            granularity=c["gran"])
+            qq, kk, vv = SA.qkv_postprocess(qkv, nw[0], nw[1], freqs, H, D, 1e-5)
+            return SA.quantize_qkv(qq, kk, vv, sm, qk=c["qk"], pv=c["pv"], granularity=c["gran"])
+
+        def step(ev=None, out_layout=layout, merge_heads=False, fused=True):
             if ev is not None:
                 ev[0].record()
-            qz = SA.quantize_qkv(qd, kd, vd, sm, qk=c["qk"], pv=c["pv"], granularity=c["gran"])
+            qz = quantize(fused)
             if ev is not None:
                 ev[1].record()
             out, _ = SA.attn_from_quantized(qz, B, H, block_mask=bmd, doc_ids=docd, out_layout=out_layout)
@@ -304,6 +325,12 @@ def all_configs(args):
                     sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps)
 
         a_ms, q_ms = timed()
+        if c.get("producer"):
+            _, sep_q_ms = timed(fused=False)
+            extra["from_qkv"] = {"producer_in_quantize_ms": round(q_ms, 5),
+                                 "producer_then_quantize_ms": round(sep_q_ms, 5),
+                                 "saved_ms": round(sep_q_ms - q_ms, 5),
+                                 "note": "quantize columns include the producer (RMSNorm + RoPE) in both forms"}
         if layout == "bnhd":
             sep_ms, _ = timed(out_layout="bhnd", merge_heads=True)
             extra["outproj_input"] = {"fused_bnhd_store_ms": round(a_ms, 5),

@@ -1,8 +1,10 @@
 """MI355X-native (gfx950) SageAttention forward for sqcu/futudiffu.
 
 Importing this package registers the ``futudiffu_ii::sage_attn_masked``,
-``futudiffu_ii::sage_attn``, ``futudiffu_ii::sage_attn_ext`` and
-``futudiffu_ii::sage_attn_masked_merged_heads`` custom ops.
+``futudiffu_ii::sage_attn``, ``futudiffu_ii::sage_attn_ext``,
+``futudiffu_ii::sage_attn_masked_merged_heads`` and
+``futudiffu_ii::sage_attn_qkv_masked`` custom ops.  ``futudiffu_amd.fused_kernels``
+(imported separately) registers ``futudiffu::fused_qkv_postprocess``.
 The compute lives in ``libsage_mi355x.so`` (HIP, built by ``build.py``).
 """
 
@@ -11,11 +13,14 @@ from .attention_srcii import (  # noqa: F401
     sage_attn_ext_op,
     sage_attn_masked_merged_heads_op,
     sage_attn_masked_op,
+    sage_attn_qkv_masked_op,
     sage_attn_op,
 )
 from .block_mask import build_block_mask, build_doc_ids  # noqa: F401
 from .sage_attention import (  # noqa: F401
     configure_sage,
+    qkv_postprocess,
+    quantize_from_qkv,
     quantize_qkv,
     sage_attn_forward,
     sage_attn_forward_masked,
@@ -23,4 +28,5 @@ from .sage_attention import (  # noqa: F401
     sage_attn_forward_masked_with_lse,
     sage_attn_forward_with_lse,
     sage_forward,
+    sage_forward_from_qkv,
 )

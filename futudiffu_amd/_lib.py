@@ -31,6 +31,10 @@ SIGNATURES = {
         _P, _I64, _I64, _I64, _P, _P, _c.c_size_t, _P, _c.c_int, _P, _P]),
     "sage_qk_int32": (_c.c_int, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "sage_build_tile_mask": (_c.c_int, [_P, _I64, _I64, _c.c_int32, _P, _P]),
+    "sage_qkv_postprocess": (_c.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_float, _P, _P, _P, _P]),
+    "sage_quantize_from_qkv": (_c.c_int, [
+        _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_float, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_float,
+        _P, _P, _P, _P, _P, _P, _P, _P, _c.c_size_t, _P]),
     "sage_doc_ids_from_cu_seqlens": (_c.c_int, [_P, _I64, _I64, _I64, _P, _P]),
 }
 

@@ -16,6 +16,9 @@ the ``configure_sage`` selection (sage_attention.py:271-341).
 output layout).  ``futudiffu_ii::sage_attn_masked_merged_heads`` is
 ``sage_attn_masked`` with the output already in the ``[B, N, H*D]`` layout of
 the out-projection that follows it (transformer.py:471).
+``futudiffu_ii::sage_attn_qkv_masked`` also takes over the q/k/v producer
+(fused_qkv_postprocess, transformer.py:459-463): it reads the QKV projection
+output and quantizes inside the producer, so bf16 q, k, v never reach HBM.
 
 Backward is not part of this forward-only build: the ops register an autograd
 formula that raises, so a training graph fails loudly instead of silently
@@ -30,6 +33,7 @@ from torch import Tensor
 
 from .sage_attention import (
     sage_attn_forward_masked_merged_heads,
+    sage_forward_from_qkv,
     sage_attn_forward_masked_with_lse,
     sage_attn_forward_with_lse,
     sage_forward,
@@ -120,3 +124,26 @@ def _fake_fwd_merged(q, k, v, block_mask, sm_scale):
 
 
 sage_attn_masked_merged_heads_op.register_autograd(_no_backward, setup_context=_setup_context)
+
+
+# JointAttention.forward (transformer.py:459-471): fused_qkv_postprocess, then
+# sage_attn_masked, then the transpose into the out-projection layout.  This
+# op does all three from the QKV projection output, with the production
+# kernel's variant (int8 QK, bf16 PV, sage_attention.py:521-529).
+@torch.library.custom_op("futudiffu_ii::sage_attn_qkv_masked", mutates_args=())
+def sage_attn_qkv_masked_op(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, freqs_cis: Tensor,
+                            block_mask: Tensor, n_heads: int, head_dim: int, norm_eps: float,
+                            sm_scale: float) -> tuple[Tensor, Tensor]:
+    out, lse = sage_forward_from_qkv(qkv, q_norm_weight, k_norm_weight, freqs_cis, n_heads, head_dim, norm_eps,
+                                     sm_scale, block_mask=block_mask, qk="int8", pv="bf16", out_layout="bnhd")
+    return out, lse
+
+
+@sage_attn_qkv_masked_op.register_fake
+def _fake_qkv_masked(qkv, q_norm_weight, k_norm_weight, freqs_cis, block_mask, n_heads, head_dim, norm_eps,
+                     sm_scale):
+    B, N = qkv.shape[0], qkv.shape[1]
+    return qkv.new_empty(B, N, n_heads * head_dim), qkv.new_empty(B * n_heads, N, dtype=torch.float32)
+
+
+sage_attn_qkv_masked_op.register_autograd(_no_backward, setup_context=_setup_context)

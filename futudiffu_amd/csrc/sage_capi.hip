@@ -56,16 +56,17 @@ size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) {
   return sage::attn_workspace_bytes(b, h, n, d);
 }
 
-int sage_quantize_qkv(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t d, int qk_kind,
-                      int pv_kind, int granularity, int smooth_k, float sm_scale_log2e, void* q_codes,
-                      float* q_scale, void* k_codes, float* k_scale, void* v_out, float* v_scale, void* k_mean,
-                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  int st = check_common(bh, n, d, qk_kind, pv_kind, granularity);
-  if (st) return st;
-  if (!q || !k || !v || !q_codes || !q_scale || !k_codes || !k_scale || !v_out)
-    return fail(SAGE_ERR_ARG, "null tensor pointer");
+}  // extern "C"
+
+namespace {
+
+// Outputs and workspace of a quantization call.
+int check_quant_outputs(int64_t bh, int64_t n, int64_t d, int pv_kind, int smooth_k, const void* q_codes,
+                        const float* q_scale, const void* k_codes, const float* k_scale, const void* v_out,
+                        const float* v_scale, const void* k_mean, const void* workspace, size_t workspace_bytes) {
+  if (!q_codes || !q_scale || !k_codes || !k_scale || !v_out) return fail(SAGE_ERR_ARG, "null tensor pointer");
   if (pv_kind == SAGE_PV_FP8 && !v_scale) return fail(SAGE_ERR_ARG, "fp8 PV needs v_scale");
-  const void* ptrs[] = {q, k, v, q_codes, q_scale, k_codes, k_scale, v_out};
+  const void* ptrs[] = {q_codes, q_scale, k_codes, k_scale, v_out};
   for (const void* p : ptrs)
     if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
   if (v_scale && !aligned16(v_scale)) return fail(SAGE_ERR_ALIGN, "v_scale must be 16-byte aligned");
@@ -76,12 +77,89 @@ int sage_quantize_qkv(const void* q, const void* k, const void* v, int64_t bh, i
       return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need, workspace_bytes);
     if (!aligned16(workspace)) return fail(SAGE_ERR_ALIGN, "workspace must be 16-byte aligned");
   }
+  return SAGE_OK;
+}
+
+// Inputs of the q/k/v producer.
+int check_producer(const void* qkv, const float* q_norm_w, const float* k_norm_w, const float* freqs, int64_t b,
+                   int64_t h, int64_t n, int64_t d, float norm_eps, sage::ProdArgs& prod) {
+  if (b <= 0 || h <= 0) return fail(SAGE_ERR_ARG, "b=%lld and h=%lld must be positive", (long long)b, (long long)h);
+  if (b * h > 65535) return fail(SAGE_ERR_ARG, "b*h=%lld exceeds the grid limit 65535", (long long)(b * h));
+  if (n <= 0) return fail(SAGE_ERR_ARG, "n=%lld must be positive", (long long)n);
+  if (n > (int64_t)1 << 24) return fail(SAGE_ERR_ARG, "n=%lld exceeds 2^24", (long long)n);
+  if (d != 64 && d != 128) return fail(SAGE_ERR_ARG, "head_dim must be 64 or 128, got %lld", (long long)d);
+  if (!qkv || !q_norm_w || !k_norm_w || !freqs) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  const void* ptrs[] = {qkv, q_norm_w, k_norm_w, freqs};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
+  if (!(norm_eps >= 0.0f)) return fail(SAGE_ERR_ARG, "norm_eps must be >= 0");
+  // one workgroup per (64-token block, head) in a 1D grid
+  if (b * h * ((n + 63) / 64) > 0x7fffffff)
+    return fail(SAGE_ERR_ARG, "b*h*ceil(n/64) = %lld exceeds the grid limit", (long long)(b * h * ((n + 63) / 64)));
+  prod = sage::ProdArgs{static_cast<const uint16_t*>(qkv), q_norm_w, k_norm_w, freqs, (int)h, (int)(b * h),
+                        norm_eps};
+  return SAGE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sage_quantize_qkv(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t d, int qk_kind,
+                      int pv_kind, int granularity, int smooth_k, float sm_scale_log2e, void* q_codes,
+                      float* q_scale, void* k_codes, float* k_scale, void* v_out, float* v_scale, void* k_mean,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = check_common(bh, n, d, qk_kind, pv_kind, granularity);
+  if (st) return st;
+  if (!q || !k || !v) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  const void* ins[] = {q, k, v};
+  for (const void* p : ins)
+    if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
+  st = check_quant_outputs(bh, n, d, pv_kind, smooth_k, q_codes, q_scale, k_codes, k_scale, v_out, v_scale, k_mean,
+                           workspace, workspace_bytes);
+  if (st) return st;
   hipError_t e = sage::launch_quantize(
       qk_kind, pv_kind, granularity, smooth_k != 0, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
       static_cast<const uint16_t*>(v), bh, n, d, sm_scale_log2e, static_cast<double*>(workspace),
       static_cast<uint8_t*>(q_codes), q_scale, static_cast<uint8_t*>(k_codes), k_scale, static_cast<uint8_t*>(v_out),
-      v_scale, static_cast<uint16_t*>(k_mean), stream);
+      v_scale, static_cast<uint16_t*>(k_mean), sage::ProdArgs{}, stream);
   return launch_status(e, "sage_quantize_qkv");
+}
+
+int sage_qkv_postprocess(const void* qkv, const float* q_norm_w, const float* k_norm_w, const float* freqs,
+                         int64_t b, int64_t h, int64_t n, int64_t d, float norm_eps, void* q_out, void* k_out,
+                         void* v_out, hipStream_t stream) {
+  sage::ProdArgs prod;
+  int st = check_producer(qkv, q_norm_w, k_norm_w, freqs, b, h, n, d, norm_eps, prod);
+  if (st) return st;
+  if (!q_out || !k_out || !v_out) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  const void* outs[] = {q_out, k_out, v_out};
+  for (const void* p : outs)
+    if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
+  return launch_status(sage::launch_qkv_postprocess(prod, b * h, n, d, static_cast<uint16_t*>(q_out),
+                                                    static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out),
+                                                    stream),
+                       "sage_qkv_postprocess");
+}
+
+int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* k_norm_w, const float* freqs,
+                           int64_t b, int64_t h, int64_t n, int64_t d, float norm_eps, int qk_kind, int pv_kind,
+                           int granularity, int smooth_k, float sm_scale_log2e, void* q_codes, float* q_scale,
+                           void* k_codes, float* k_scale, void* v_out, float* v_scale, void* k_mean, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+  sage::ProdArgs prod;
+  int st = check_producer(qkv, q_norm_w, k_norm_w, freqs, b, h, n, d, norm_eps, prod);
+  if (st) return st;
+  st = check_common(b * h, n, d, qk_kind, pv_kind, granularity);
+  if (st) return st;
+  st = check_quant_outputs(b * h, n, d, pv_kind, smooth_k, q_codes, q_scale, k_codes, k_scale, v_out, v_scale,
+                           k_mean, workspace, workspace_bytes);
+  if (st) return st;
+  hipError_t e = sage::launch_quantize(
+      qk_kind, pv_kind, granularity, smooth_k != 0, nullptr, nullptr, nullptr, b * h, n, d, sm_scale_log2e,
+      static_cast<double*>(workspace), static_cast<uint8_t*>(q_codes), q_scale, static_cast<uint8_t*>(k_codes),
+      k_scale, static_cast<uint8_t*>(v_out), v_scale, static_cast<uint16_t*>(k_mean), prod, stream);
+  return launch_status(e, "sage_quantize_from_qkv");
 }
 
 int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,

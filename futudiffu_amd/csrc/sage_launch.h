@@ -76,10 +76,26 @@ inline TailSplit tail_split(int64_t n_items, int64_t nt) {
   return t;
 }
 
+// Inputs of the q/k/v producer (QKV split + per-head RMSNorm + Flux RoPE +
+// transpose, fused_kernels.py:271-390).  With qkv set, the quantization reads
+// the projection output and applies the producer itself; with qkv null it
+// reads bf16 q, k, v [BH, N, D].
+struct ProdArgs {
+  const uint16_t* qkv;  // bf16 [B, N, 3*H*D]
+  const float* qw;      // RMSNorm weights of q and k, fp32 [D]
+  const float* kw;
+  const float* freqs;   // fp32 [B*N, D/2, 2, 2]: [[cos, -sin], [sin, cos]] per channel pair
+  int h;
+  int bh;               // B*H
+  float eps;
+};
+
 hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t* q, const uint16_t* k,
                            const uint16_t* v, int64_t bh, int64_t n, int64_t d, float fold, double* ws,
                            uint8_t* qc, float* qs, uint8_t* kc, float* ks, uint8_t* vout, float* vs,
-                           uint16_t* kmean, hipStream_t st);
+                           uint16_t* kmean, const ProdArgs& prod, hipStream_t st);
+hipError_t launch_qkv_postprocess(const ProdArgs& prod, int64_t bh, int64_t n, int64_t d, uint16_t* q_out,
+                                  uint16_t* k_out, uint16_t* v_out, hipStream_t st);
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
 
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb, hipStream_t st);

@@ -113,6 +113,172 @@ __device__ __forceinline__ void row_amax(const float (&x)[PASSES][8], float (&am
   }
 }
 
+// ---- q/k producer (fused_qkv_postprocess, fused_kernels.py:271-390) ---------
+
+// Sum over the LPR consecutive lanes (8 or 16) that hold one token's channels:
+// a pairwise tree over the lanes in order, with DPP moves of the two halves of
+// the fp64 value (quad xor 1, quad xor 2, half-row mirror, row mirror, as in
+// group_max).  At each step both lanes of a pair add the same two operands, so
+// every lane of the token ends with the same value.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+template <int LPR>
+__device__ __forceinline__ double token_sum(double v) {
+  v += dpp_f64<0xB1>(v);   // [1,0,3,2]
+  v += dpp_f64<0x4E>(v);   // [2,3,0,1]
+  v += dpp_f64<0x141>(v);  // half-row mirror: quad q with quad q^1
+  if constexpr (LPR == 16) v += dpp_f64<0x140>(v);  // row mirror: half-row with half-row
+  return v;
+}
+
+// Two fp32 -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32) in one word.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// RMSNorm + rotary embedding of the 8 channels [8*c8, +8) of one token held
+// by a lane (bf16 in, bf16 out).  rrms = 1 / sqrt(mean(x^2) + eps) over the
+// token's D channels (fused_kernels.py:316-320; the sum of squares in fp64, in
+// a fixed order: each lane's 8 channels left to right, then a pairwise tree
+// over the token's lanes; rounded once to fp32), n = x * rrms * w (:357-360), and per channel
+// pair (2p, 2p+1) with fr[p] = (cos, -sin, sin, cos) (:334-336):
+// even' = cos*n_even + (-sin)*n_odd, odd' = sin*n_even + cos*n_odd (:363-366),
+// every product and sum a separately rounded fp32 operation.
+template <int D>
+__device__ __forceinline__ uint4 rms_rope8(uint4 w, const float (&nw)[8], const f32x4 (&fr)[4], float eps) {
+#pragma clang fp contract(off)  // no fused multiply-add: every product and sum rounds on its own
+  float x[8];
+  unpack8(w, x);
+  double ss = 0.0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = __builtin_fma((double)x[e], (double)x[e], ss);  // the square is exact
+  ss = token_sum<D / 8>(ss);
+  const float ms = (float)(ss / (double)D);
+  const float rrms = 1.0f / sqrtf(ms + eps);  // correctly rounded sqrt and division
+  float nn[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) nn[e] = (x[e] * rrms) * nw[e];
+  uint32_t o[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float re = fr[p][0] * nn[2 * p] + fr[p][1] * nn[2 * p + 1];
+    const float ro = fr[p][2] * nn[2 * p] + fr[p][0] * nn[2 * p + 1];
+    o[p] = pack_bf16x2(re, ro);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// The rotary matrices of channel pairs [4*c8, +4) of token `row` of the
+// flattened (batch, token) axis.
+template <int D>
+__device__ __forceinline__ void load_freqs(const float* freqs, int64_t row, int c8, f32x4 (&fr)[4]) {
+  const f32x4* fp = reinterpret_cast<const f32x4*>(freqs + (row * (D / 2) + 4 * c8) * 4);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) fr[p] = fp[p];
+}
+
+__device__ __forceinline__ void load_w8(const float* w, int c8, float (&out)[8]) {
+  const f32x4* p = reinterpret_cast<const f32x4*>(w + 8 * c8);
+  const f32x4 a = p[0], b = p[1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[i] = a[i];
+    out[4 + i] = b[i];
+  }
+}
+
+// Block coordinates (unit, bh).  Reading bf16 q, k, v [BH, N, D], the 2D grid
+// (units, BH) walks one head's units.  The projection output [B, N, 3*H*D]
+// holds every head in each token row, so producer launches use a 1D grid with
+// the head fastest: consecutive workgroups read all heads of the same rows.
+template <bool PROD>
+__device__ __forceinline__ void block_coords(const ProdArgs& prod, int64_t& unit, int& bh) {
+  if constexpr (PROD) {
+    const int64_t b = blockIdx.x;
+    unit = b / prod.bh;
+    bh = (int)(b - unit * prod.bh);
+  } else {
+    unit = blockIdx.x;
+    bh = (int)blockIdx.y;
+  }
+}
+
+// Source rows of one head for the quantization: bf16 q, k, v [BH, N, D], or
+// (PROD) the q, k and v column blocks of head bh % h in the projection output
+// [B, N, 3*h*D], whose tokens are 3*h*D elements apart.
+template <int D, bool PROD>
+struct HeadRows {
+  const uint16_t *q, *k, *v;
+  int64_t stride;  // elements between consecutive tokens
+  int64_t row0;    // flattened (batch, token) index of token 0 (freqs row)
+  __device__ HeadRows(const uint16_t* q_, const uint16_t* k_, const uint16_t* v_, const ProdArgs& prod, int bh,
+                      int64_t n) {
+    if constexpr (PROD) {
+      const int b = bh / prod.h, head = bh - b * prod.h;
+      stride = 3LL * prod.h * D;
+      row0 = (int64_t)b * n;
+      q = prod.qkv + row0 * stride + (int64_t)head * D;
+      k = q + (int64_t)prod.h * D;
+      v = k + (int64_t)prod.h * D;
+    } else {
+      stride = D;
+      row0 = 0;
+      q = q_ + (int64_t)bh * n * D;
+      k = k_ + (int64_t)bh * n * D;
+      v = v_ + (int64_t)bh * n * D;
+    }
+  }
+};
+
+// Standalone producer: bf16 q, k, v [BH, N, D] from the projection output
+// (the outputs of fused_qkv_postprocess, fused_kernels.py:372-385).  One
+// workgroup per (64-token block, bh); lane (rr, c8) holds channels
+// [8*c8, +8) of tokens rr + RPP*ps.
+template <int D>
+__global__ void __launch_bounds__(256) qkv_postprocess_kernel(ProdArgs prod, int64_t n, uint16_t* __restrict__ q_out,
+                                                              uint16_t* __restrict__ k_out,
+                                                              uint16_t* __restrict__ v_out) {
+  constexpr int LPR = D / 8;
+  constexpr int RPP = 256 / LPR;
+  constexpr int PASSES = 64 / RPP;
+  int64_t unit;
+  int bh;
+  block_coords<true>(prod, unit, bh);
+  const int tid = threadIdx.x;
+  const int c8 = tid % LPR, rr = tid / LPR;
+  const int64_t tok0 = unit * 64;
+  const HeadRows<D, true> src(nullptr, nullptr, nullptr, prod, bh, n);
+  float qn[8], kn[8];
+  load_w8(prod.qw, c8, qn);
+  load_w8(prod.kw, c8, kn);
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int64_t t = tok0 + rr + ps * RPP;
+    const int64_t tok = min(t, n - 1);  // clamped: the lanes of a token reduce together
+    const uint4 qw = *reinterpret_cast<const uint4*>(src.q + tok * src.stride + c8 * 8);
+    const uint4 kw = *reinterpret_cast<const uint4*>(src.k + tok * src.stride + c8 * 8);
+    const uint4 vw = *reinterpret_cast<const uint4*>(src.v + tok * src.stride + c8 * 8);
+    f32x4 fr[4];
+    load_freqs<D>(prod.freqs, src.row0 + tok, c8, fr);
+    const uint4 qo = rms_rope8<D>(qw, qn, fr, prod.eps);
+    const uint4 ko = rms_rope8<D>(kw, kn, fr, prod.eps);
+    if (t < n) {
+      const int64_t o = ((int64_t)bh * n + t) * D + c8 * 8;
+      *reinterpret_cast<uint4*>(q_out + o) = qo;
+      *reinterpret_cast<uint4*>(k_out + o) = ko;
+      *reinterpret_cast<uint4*>(v_out + o) = vw;
+    }
+  }
+}
+
 // Tokens per K column-sum chunk.
 constexpr int kSumTokens = 256;
 
@@ -121,34 +287,53 @@ __host__ __device__ inline int64_t k_sum_chunks(int64_t n) { return (n + kSumTok
 // Smoothing pass 1: fp64 column sums of K over each 256-token chunk of each
 // head, part[bh][chunk][d].  One workgroup per (chunk, bh); lane (rr, c8)
 // holds channels [8*c8, +8) of tokens rr + RPP*ps.  Every sum is formed in a
-// fixed order, so the result does not depend on scheduling.
-template <int D>
+// fixed order, so the result does not depend on scheduling.  PROD: K comes
+// from the projection output through the producer (RMSNorm + rotary), four
+// tokens per lane at a time.
+template <int D, bool PROD>
 __global__ void __launch_bounds__(256) k_colsum_kernel(const uint16_t* __restrict__ k, int64_t n,
-                                                       double* __restrict__ part) {
+                                                       double* __restrict__ part, ProdArgs prod) {
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   constexpr int PASSES = kSumTokens / RPP;
+  constexpr int GROUP = PROD ? 4 : PASSES;  // tokens per lane loaded together
   __shared__ double ksw[4][D];
-  const int bh = blockIdx.y, ch = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
+  int64_t ch;
+  int bh;
+  block_coords<PROD>(prod, ch, bh);
+  const int tid = threadIdx.x, wave = tid >> 6;
   const int c8 = tid % LPR, rr = tid / LPR;
   const int64_t tok0 = (int64_t)ch * kSumTokens;
-  const uint16_t* kb = k + (int64_t)bh * n * D + c8 * 8;
-  uint4 w[PASSES];
-#pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) {
-    const int64_t tok = min(tok0 + rr + ps * RPP, n - 1);  // clamped in bounds, masked below
-    w[ps] = *reinterpret_cast<const uint4*>(kb + tok * D);
-  }
+  const HeadRows<D, PROD> src(k, k, k, prod, bh, n);
+  float kn[8];
+  if constexpr (PROD) load_w8(prod.kw, c8, kn);
   double cs[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) cs[e] = 0.0;
+#pragma unroll 1
+  for (int g0 = 0; g0 < PASSES; g0 += GROUP) {
+    uint4 w[GROUP];
 #pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) {
-    float x[8];
-    unpack8(w[ps], x);
-    const bool keep = tok0 + rr + ps * RPP < n;
+    for (int i = 0; i < GROUP; ++i) {
+      const int64_t tok = min(tok0 + rr + (g0 + i) * RPP, n - 1);  // clamped in bounds, masked below
+      w[i] = *reinterpret_cast<const uint4*>(src.k + tok * src.stride + c8 * 8);
+    }
+    if constexpr (PROD) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) cs[e] += keep ? (double)x[e] : 0.0;
+      for (int i = 0; i < GROUP; ++i) {
+        f32x4 fr[4];
+        load_freqs<D>(prod.freqs, src.row0 + min(tok0 + rr + (g0 + i) * RPP, n - 1), c8, fr);
+        w[i] = rms_rope8<D>(w[i], kn, fr, prod.eps);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < GROUP; ++i) {
+      float x[8];
+      unpack8(w[i], x);
+      const bool keep = tok0 + rr + (g0 + i) * RPP < n;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cs[e] += keep ? (double)x[e] : 0.0;
+    }
   }
   // token rows of the wave (lanes c8 + LPR*m), then the 4 waves
 #pragma unroll
@@ -161,7 +346,7 @@ __global__ void __launch_bounds__(256) k_colsum_kernel(const uint16_t* __restric
   }
   __syncthreads();
   if (tid < D)
-    part[((int64_t)bh * gridDim.x + ch) * D + tid] = (ksw[0][tid] + ksw[1][tid]) + (ksw[2][tid] + ksw[3][tid]);
+    part[((int64_t)bh * k_sum_chunks(n) + ch) * D + tid] = (ksw[0][tid] + ksw[1][tid]) + (ksw[2][tid] + ksw[3][tid]);
 }
 
 // One workgroup per (64-token block, bh).
@@ -170,13 +355,15 @@ __global__ void __launch_bounds__(256) k_colsum_kernel(const uint16_t* __restric
 //         4g..4g+3, so the 4 codes of a channel form one 32-bit fragment word.
 // With smoothing, the head's mean is the sum of its chunk sums (fixed order)
 // / N in fp64, rounded to fp32 then bf16 (the reference's bf16 mean), and K
-// rows are smoothed as bf16(k - mean).
-template <int D, int QK, int PV, int GRAN, bool SMOOTH>
+// rows are smoothed as bf16(k - mean).  PROD: q, k and v come from the
+// projection output, q and k through the producer (RMSNorm + rotary), so the
+// codes equal those of the producer's bf16 outputs.
+template <int D, int QK, int PV, int GRAN, bool SMOOTH, bool PROD>
 __global__ void __launch_bounds__(256) quantize_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     int64_t n, int64_t np, float fold, const double* __restrict__ ksum_part,
     uint8_t* __restrict__ qc, float* __restrict__ qs, uint8_t* __restrict__ kc, float* __restrict__ ks,
-    uint8_t* __restrict__ vout, float* __restrict__ vs, uint16_t* __restrict__ kmean) {
+    uint8_t* __restrict__ vout, float* __restrict__ vs, uint16_t* __restrict__ kmean, ProdArgs prod) {
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   constexpr int PASSES = 64 / RPP;
@@ -191,10 +378,13 @@ __global__ void __launch_bounds__(256) quantize_kernel(
   // V operand image of this 64-token block in fragment order; written to
   // global as contiguous 16-byte chunks
   __shared__ __attribute__((aligned(16))) uint8_t vimg[(PV == kPV_FP8 ? 1 : 2) * 64 * D];
-  const int bh = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
+  int64_t blk;
+  int bh;
+  block_coords<PROD>(prod, blk, bh);
+  const int tid = threadIdx.x, wave = tid >> 6;
   const int c8 = tid % LPR, rr = tid / LPR;
   const int64_t tok0 = (int64_t)blk * 64;
-  const int64_t so = (int64_t)bh * n * D;
+  const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
   const int64_t co = (int64_t)bh * np * D;
   const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
 
@@ -219,14 +409,27 @@ __global__ void __launch_bounds__(256) quantize_kernel(
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
     const int64_t tok = min(tok0 + rr + ps * RPP, n - 1);
-    qw[ps] = *reinterpret_cast<const uint4*>(q + so + tok * D + c8 * 8);
-    kw[ps] = *reinterpret_cast<const uint4*>(k + so + tok * D + c8 * 8);
+    qw[ps] = *reinterpret_cast<const uint4*>(src.q + tok * src.stride + c8 * 8);
+    kw[ps] = *reinterpret_cast<const uint4*>(src.k + tok * src.stride + c8 * 8);
   }
   const int g = (tid / LPR) & 15;  // V token group (V work only for tid < VTHREADS)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t tok = min(tok0 + 4 * g + i, n - 1);
-    vw[i] = *reinterpret_cast<const uint4*>(v + so + tok * D + c8 * 8);
+    vw[i] = *reinterpret_cast<const uint4*>(src.v + tok * src.stride + c8 * 8);
+  }
+  if constexpr (PROD) {
+    // the producer's bf16 q and k (every lane of a token takes part in its sum)
+    float qn[8], kn[8];
+    load_w8(prod.qw, c8, qn);
+    load_w8(prod.kw, c8, kn);
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      f32x4 fr[4];
+      load_freqs<D>(prod.freqs, src.row0 + min(tok0 + rr + ps * RPP, n - 1), c8, fr);
+      qw[ps] = rms_rope8<D>(qw[ps], qn, fr, prod.eps);
+      kw[ps] = rms_rope8<D>(kw[ps], kn, fr, prod.eps);
+    }
   }
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
@@ -382,40 +585,51 @@ __global__ void __launch_bounds__(256) quantize_kernel(
   }
 }
 
-template <int D, int QK, int PV, int GRAN, bool SMOOTH>
-hipError_t launch_quantize_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t bh, int64_t n,
-                             float fold, double* ws, uint8_t* qc, float* qs, uint8_t* kc, float* ks,
-                             uint8_t* vout, float* vs, uint16_t* kmean, hipStream_t st) {
-  const int64_t np = padded_len(n);
+// Arguments of one quantization call.
+struct QuantCall {
+  const uint16_t *q, *k, *v;
+  int64_t bh, n;
+  float fold;
+  double* ws;
+  uint8_t* qc;
+  float* qs;
+  uint8_t* kc;
+  float* ks;
+  uint8_t* vout;
+  float* vs;
+  uint16_t* kmean;
+  ProdArgs prod;
+};
+
+template <int D, int QK, int PV, int GRAN, bool SMOOTH, bool PROD>
+hipError_t launch_quantize_t(const QuantCall& a, hipStream_t st) {
+  const int64_t np = padded_len(a.n);
   const int nblk = (int)(np / 64);
   if (SMOOTH) {
-    hipLaunchKernelGGL(k_colsum_kernel<D>, dim3((unsigned)k_sum_chunks(n), (unsigned)bh), dim3(256), 0, st, k, n,
-                       ws);
+    const int64_t nch = k_sum_chunks(a.n);
+    const dim3 g = PROD ? dim3((unsigned)(nch * a.bh)) : dim3((unsigned)nch, (unsigned)a.bh);
+    hipLaunchKernelGGL((k_colsum_kernel<D, PROD>), g, dim3(256), 0, st, a.k, a.n, a.ws, a.prod);
   }
-  hipLaunchKernelGGL((quantize_kernel<D, QK, PV, GRAN, SMOOTH>), dim3((unsigned)nblk, (unsigned)bh), dim3(256), 0,
-                     st, q, k, v, n, np, fold, ws, qc, qs, kc, ks, vout, vs, kmean);
+  const dim3 grid = PROD ? dim3((unsigned)((int64_t)nblk * a.bh)) : dim3((unsigned)nblk, (unsigned)a.bh);
+  hipLaunchKernelGGL((quantize_kernel<D, QK, PV, GRAN, SMOOTH, PROD>), grid, dim3(256), 0, st, a.q, a.k, a.v, a.n, np, a.fold, a.ws, a.qc, a.qs, a.kc, a.ks, a.vout, a.vs,
+                     a.kmean, a.prod);
   return hipGetLastError();
 }
 
 template <int D, int QK, int PV, int GRAN>
-hipError_t launch_quantize_s(bool smooth, const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t bh,
-                             int64_t n, float fold, double* ws, uint8_t* qc, float* qs, uint8_t* kc, float* ks,
-                             uint8_t* vout, float* vs, uint16_t* kmean, hipStream_t st) {
-  return smooth ? launch_quantize_t<D, QK, PV, GRAN, true>(q, k, v, bh, n, fold, ws, qc, qs, kc, ks, vout, vs,
-                                                           kmean, st)
-                : launch_quantize_t<D, QK, PV, GRAN, false>(q, k, v, bh, n, fold, ws, qc, qs, kc, ks, vout,
-                                                            vs, kmean, st);
+hipError_t launch_quantize_s(bool smooth, const QuantCall& a, hipStream_t st) {
+  const bool prod = a.prod.qkv != nullptr;
+  if (smooth)
+    return prod ? launch_quantize_t<D, QK, PV, GRAN, true, true>(a, st)
+                : launch_quantize_t<D, QK, PV, GRAN, true, false>(a, st);
+  return prod ? launch_quantize_t<D, QK, PV, GRAN, false, true>(a, st)
+              : launch_quantize_t<D, QK, PV, GRAN, false, false>(a, st);
 }
 
 template <int D>
-hipError_t launch_quantize_d(int qk, int pv, int gran, bool smooth, const uint16_t* q, const uint16_t* k,
-                             const uint16_t* v, int64_t bh, int64_t n, float fold, double* ws, uint8_t* qc,
-                             float* qs, uint8_t* kc, float* ks, uint8_t* vout, float* vs, uint16_t* kmean,
-                             hipStream_t st) {
-#define SAGE_Q_CASE(QK_, PV_, G_)                                                                        \
-  if (qk == QK_ && pv == PV_ && gran == G_)                                                              \
-    return launch_quantize_s<D, QK_, PV_, G_>(smooth, q, k, v, bh, n, fold, ws, qc, qs, kc, ks, vout, vs, \
-                                              kmean, st);
+hipError_t launch_quantize_d(int qk, int pv, int gran, bool smooth, const QuantCall& a, hipStream_t st) {
+#define SAGE_Q_CASE(QK_, PV_, G_) \
+  if (qk == QK_ && pv == PV_ && gran == G_) return launch_quantize_s<D, QK_, PV_, G_>(smooth, a, st);
   SAGE_Q_CASE(0, 0, 0) SAGE_Q_CASE(0, 0, 1) SAGE_Q_CASE(0, 1, 0) SAGE_Q_CASE(0, 1, 1)
   SAGE_Q_CASE(1, 0, 0) SAGE_Q_CASE(1, 0, 1) SAGE_Q_CASE(1, 1, 0) SAGE_Q_CASE(1, 1, 1)
 #undef SAGE_Q_CASE
@@ -425,14 +639,23 @@ hipError_t launch_quantize_d(int qk, int pv, int gran, bool smooth, const uint16
 hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t* q, const uint16_t* k,
                            const uint16_t* v, int64_t bh, int64_t n, int64_t d, float fold, double* ws,
                            uint8_t* qc, float* qs, uint8_t* kc, float* ks, uint8_t* vout, float* vs,
-                           uint16_t* kmean, hipStream_t st) {
-  if (d == 128)
-    return launch_quantize_d<128>(qk, pv, gran, smooth, q, k, v, bh, n, fold, ws, qc, qs, kc, ks, vout, vs, kmean,
-                                  st);
-  if (d == 64)
-    return launch_quantize_d<64>(qk, pv, gran, smooth, q, k, v, bh, n, fold, ws, qc, qs, kc, ks, vout, vs, kmean,
-                                 st);
+                           uint16_t* kmean, const ProdArgs& prod, hipStream_t st) {
+  const QuantCall a{q, k, v, bh, n, fold, ws, qc, qs, kc, ks, vout, vs, kmean, prod};
+  if (d == 128) return launch_quantize_d<128>(qk, pv, gran, smooth, a, st);
+  if (d == 64) return launch_quantize_d<64>(qk, pv, gran, smooth, a, st);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_qkv_postprocess(const ProdArgs& prod, int64_t bh, int64_t n, int64_t d, uint16_t* q_out,
+                                  uint16_t* k_out, uint16_t* v_out, hipStream_t st) {
+  const dim3 grid((unsigned)((n + 63) / 64 * bh));  // head fastest (block_coords)
+  if (d == 128)
+    hipLaunchKernelGGL(qkv_postprocess_kernel<128>, grid, dim3(256), 0, st, prod, n, q_out, k_out, v_out);
+  else if (d == 64)
+    hipLaunchKernelGGL(qkv_postprocess_kernel<64>, grid, dim3(256), 0, st, prod, n, q_out, k_out, v_out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 // fp64 column sums of K per head and 256-token chunk, [bh][ceil(n/256)][d].

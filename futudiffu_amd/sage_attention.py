@@ -104,20 +104,12 @@ class SageQuantized:
     d: int
 
 
-def quantize_qkv(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None, *,
-                 qk: str = "int8", pv: str = "bf16", granularity: str = "token",
-                 smooth_k: bool = True) -> SageQuantized:
-    """Smoothing + quantization of q, k, v (``[B, H, N, D]`` bf16) on the GPU."""
-    B, H, N, D = _check_inputs(q, k, v)
+def _quant_outputs(BH: int, N: int, D: int, qk: str, pv: str, granularity: str, smooth_k: bool, dev):
+    """Device buffers of one quantization call (codes in fragment order, scales, mean, workspace)."""
     if qk not in _QK or pv not in _PV or granularity not in _GRAN:
         raise ValueError(f"bad variant qk={qk!r} pv={pv!r} granularity={granularity!r}")
-    if sm_scale is None:
-        sm_scale = 1.0 / math.sqrt(D)
     lib = _lib.load()
-    BH = B * H
     Np = int(lib.sage_padded_len(N))
-    dev = q.device
-    q3, k3, v3 = (t.reshape(BH, N, D).contiguous() for t in (q, k, v))
     ns = Np if granularity == "token" else Np // 64
     qc = torch.empty(BH, Np * D, dtype=torch.uint8, device=dev)
     kc = torch.empty_like(qc)
@@ -132,13 +124,98 @@ def quantize_qkv(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None,
     km = torch.empty(BH, D, dtype=torch.bfloat16, device=dev) if smooth_k else None
     wsb = int(lib.sage_quant_workspace_bytes(BH, N, D)) if smooth_k else 0
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev) if smooth_k else None
-    fold = float(torch.tensor(sm_scale * _LOG2E, dtype=torch.float32))
+    qz = SageQuantized(qc, qs, kc, ks, vop, vs, km, qk, pv, granularity, N, Np, D)
+    return qz, ws, wsb
+
+
+def _fold(sm_scale: float) -> float:
+    """``sm_scale*log2(e)`` as the fp32 the kernels receive (sage_attention.py:493-495)."""
+    return float(torch.tensor(sm_scale * _LOG2E, dtype=torch.float32))
+
+
+def quantize_qkv(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None, *,
+                 qk: str = "int8", pv: str = "bf16", granularity: str = "token",
+                 smooth_k: bool = True) -> SageQuantized:
+    """Smoothing + quantization of q, k, v (``[B, H, N, D]`` bf16) on the GPU."""
+    B, H, N, D = _check_inputs(q, k, v)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    BH = B * H
+    dev = q.device
+    qz, ws, wsb = _quant_outputs(BH, N, D, qk, pv, granularity, smooth_k, dev)
+    q3, k3, v3 = (t.reshape(BH, N, D).contiguous() for t in (q, k, v))
+    lib = _lib.load()
     _lib.check(lib.sage_quantize_qkv(
         q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), BH, N, D,
-        _QK[qk], _PV[pv], _GRAN[granularity], int(smooth_k), fold,
-        qc.data_ptr(), qs.data_ptr(), kc.data_ptr(), ks.data_ptr(),
-        vop.data_ptr(), _ptr(vs), _ptr(km), _ptr(ws), wsb, _stream_handle(dev)))
-    return SageQuantized(qc, qs, kc, ks, vop, vs, km, qk, pv, granularity, N, Np, D)
+        _QK[qk], _PV[pv], _GRAN[granularity], int(smooth_k), _fold(sm_scale),
+        qz.q_codes.data_ptr(), qz.q_scale.data_ptr(), qz.k_codes.data_ptr(), qz.k_scale.data_ptr(),
+        qz.v_op.data_ptr(), _ptr(qz.v_scale), _ptr(qz.k_mean), _ptr(ws), wsb, _stream_handle(dev)))
+    return qz
+
+
+def _check_producer(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, freqs_cis: Tensor,
+                    n_heads: int, head_dim: int):
+    """Validation of fused_qkv_postprocess's inputs (fused_kernels.py:415-440) and
+    their device forms: fp32 weights, rotary matrices as ``[B*N, D/2, 2, 2]``."""
+    assert qkv.ndim == 3, f"Expected qkv to be 3D (B, seq, 3*dim), got {qkv.ndim}D"
+    assert qkv.is_contiguous(), "QKV must be contiguous"
+    B, N, total = qkv.shape
+    dim = n_heads * head_dim
+    assert total == 3 * dim, f"QKV last dim {total} != 3 * {dim}"
+    assert head_dim in (64, 128), f"SageAttention on MI355X requires head_dim 64 or 128, got {head_dim}"
+    assert qkv.dtype == torch.bfloat16, f"Expected BF16 input, got {qkv.dtype} for qkv"
+    if not qkv.is_cuda:
+        raise ValueError(f"qkv must be a GPU tensor (device {qkv.device})")
+    assert q_norm_weight.shape == (head_dim,), f"q_norm shape {q_norm_weight.shape} != ({head_dim},)"
+    assert k_norm_weight.shape == (head_dim,), f"k_norm shape {k_norm_weight.shape} != ({head_dim},)"
+    n_pairs = head_dim // 2
+    if freqs_cis.ndim == 6:
+        assert freqs_cis.shape[2] == 1, f"Expected freqs_cis dim 2 to be 1, got {freqs_cis.shape[2]}"
+        freqs_cis = freqs_cis.squeeze(2)
+    elif freqs_cis.ndim != 5:
+        raise ValueError(f"Unexpected freqs_cis ndim: {freqs_cis.ndim}, shape: {tuple(freqs_cis.shape)}")
+    fr = freqs_cis.reshape(B * N, n_pairs, 2, 2).to(device=qkv.device, dtype=torch.float32).contiguous()
+    qw = q_norm_weight.to(device=qkv.device, dtype=torch.float32).contiguous()
+    kw = k_norm_weight.to(device=qkv.device, dtype=torch.float32).contiguous()
+    return B, N, qw, kw, fr
+
+
+def qkv_postprocess(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, freqs_cis: Tensor,
+                    n_heads: int, head_dim: int, norm_eps: float = 1e-5) -> tuple[Tensor, Tensor, Tensor]:
+    """QKV split + per-head RMSNorm + Flux RoPE + transpose on the GPU: bf16
+    ``q, k, v`` ``[B, H, N, D]`` from the projection output ``[B, N, 3*H*D]``
+    (fused_qkv_postprocess, fused_kernels.py:271-390)."""
+    B, N, qw, kw, fr = _check_producer(qkv, q_norm_weight, k_norm_weight, freqs_cis, n_heads, head_dim)
+    out = [torch.empty(B, n_heads, N, head_dim, dtype=torch.bfloat16, device=qkv.device) for _ in range(3)]
+    lib = _lib.load()
+    _lib.check(lib.sage_qkv_postprocess(
+        qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), fr.data_ptr(), B, n_heads, N, head_dim, float(norm_eps),
+        out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(), _stream_handle(qkv.device)))
+    return out[0], out[1], out[2]
+
+
+def quantize_from_qkv(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, freqs_cis: Tensor,
+                      n_heads: int, head_dim: int, norm_eps: float = 1e-5, sm_scale: float | None = None, *,
+                      qk: str = "int8", pv: str = "bf16", granularity: str = "token",
+                      smooth_k: bool = True) -> SageQuantized:
+    """The quantized operands of ``qkv_postprocess``'s q, k, v, straight from the
+    projection output: the producer (RMSNorm + RoPE) runs inside the
+    quantization kernels, so the bf16 q, k, v never reach HBM.  Bit-identical
+    to ``quantize_qkv(*qkv_postprocess(...))``."""
+    B, N, qw, kw, fr = _check_producer(qkv, q_norm_weight, k_norm_weight, freqs_cis, n_heads, head_dim)
+    D = head_dim
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    BH = B * n_heads
+    dev = qkv.device
+    qz, ws, wsb = _quant_outputs(BH, N, D, qk, pv, granularity, smooth_k, dev)
+    lib = _lib.load()
+    _lib.check(lib.sage_quantize_from_qkv(
+        qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), fr.data_ptr(), B, n_heads, N, D, float(norm_eps),
+        _QK[qk], _PV[pv], _GRAN[granularity], int(smooth_k), _fold(sm_scale),
+        qz.q_codes.data_ptr(), qz.q_scale.data_ptr(), qz.k_codes.data_ptr(), qz.k_scale.data_ptr(),
+        qz.v_op.data_ptr(), _ptr(qz.v_scale), _ptr(qz.k_mean), _ptr(ws), wsb, _stream_handle(dev)))
+    return qz
 
 
 def _norm_mask(block_mask: Tensor | None, BH: int, N: int, device) -> tuple[Tensor | None, int, int, int]:
@@ -222,6 +299,23 @@ def sage_forward(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None,
         raise ValueError(f"out_layout must be one of {sorted(_LAYOUT)}, got {out_layout!r}")
     qz = quantize_qkv(q, k, v, sm_scale, qk=qk, pv=pv, granularity=granularity, smooth_k=smooth_k)
     return attn_from_quantized(qz, B, H, block_mask=block_mask, doc_ids=doc_ids, out_layout=out_layout)
+
+
+def sage_forward_from_qkv(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, freqs_cis: Tensor,
+                          n_heads: int, head_dim: int, norm_eps: float = 1e-5, sm_scale: float | None = None, *,
+                          block_mask: Tensor | None = None, doc_ids: Tensor | None = None, qk: str = "int8",
+                          pv: str = "bf16", granularity: str = "token", smooth_k: bool = True,
+                          out_layout: str = "bnhd") -> tuple[Tensor, Tensor]:
+    """JointAttention's attention from the QKV projection output
+    (transformer.py:459-471): producer, quantization and attention, returning
+    ``out`` in ``[B, N, H*D]`` (``out_layout="bnhd"``, the out-projection input)
+    or ``[B, H, N, D]``, and ``lse`` ``[B*H, N]``."""
+    if out_layout not in _LAYOUT:
+        raise ValueError(f"out_layout must be one of {sorted(_LAYOUT)}, got {out_layout!r}")
+    qz = quantize_from_qkv(qkv, q_norm_weight, k_norm_weight, freqs_cis, n_heads, head_dim, norm_eps, sm_scale,
+                           qk=qk, pv=pv, granularity=granularity, smooth_k=smooth_k)
+    return attn_from_quantized(qz, qkv.shape[0], n_heads, block_mask=block_mask, doc_ids=doc_ids,
+                               out_layout=out_layout)
 
 
 def sage_attn_forward(q: Tensor, k: Tensor, v: Tensor, sm_scale: float | None = None) -> Tensor:

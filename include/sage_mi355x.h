@@ -112,6 +112,40 @@ int sage_quantize_qkv(const void* q, const void* k, const void* v,
                       void* workspace, size_t workspace_bytes,
                       hipStream_t stream);
 
+/* The q/k/v producer: QKV split + per-head RMSNorm + Flux RoPE + transpose.
+ * Replaces fused_qkv_postprocess (src/futudiffu/fused_kernels.py:271-390,
+ * op :613-643).
+ *   qkv        bf16 [B, N, 3*H*D] (the QKV projection output).
+ *   q_norm_w,
+ *   k_norm_w   fp32 [D] RMSNorm weights.
+ *   freqs      fp32 [B*N, D/2, 2, 2] rotary matrices [[cos, -sin], [sin, cos]].
+ *   q_out,
+ *   k_out,
+ *   v_out      bf16 [B, H, N, D].
+ * q' = rope(x * rrms * w) with rrms = 1 / sqrt(mean(x^2) + norm_eps) per
+ * token and head; the sum of squares is exact (fp64) and every other step a
+ * separately rounded fp32 operation, so results are reproducible bit for bit.
+ * V is copied unchanged.  All pointers 16-byte aligned. */
+int sage_qkv_postprocess(const void* qkv, const float* q_norm_w, const float* k_norm_w,
+                         const float* freqs, int64_t b, int64_t h, int64_t n, int64_t d,
+                         float norm_eps, void* q_out, void* k_out, void* v_out,
+                         hipStream_t stream);
+
+/* sage_quantize_qkv applied to the outputs of sage_qkv_postprocess, without
+ * writing them: the producer runs inside the quantization kernels, which read
+ * the projection output directly (half the HBM traffic of producer +
+ * quantization).  Outputs are bit-identical to that two-call sequence.  No
+ * reference counterpart (the reference writes bf16 q, k, v, fused_kernels.py
+ * :372-385, and its attention quantizes them again).  Same outputs, workspace
+ * and kinds as sage_quantize_qkv with bh = b*h. */
+int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* k_norm_w,
+                           const float* freqs, int64_t b, int64_t h, int64_t n, int64_t d,
+                           float norm_eps, int qk_kind, int pv_kind, int granularity,
+                           int smooth_k, float sm_scale_log2e,
+                           void* q_codes, float* q_scale, void* k_codes, float* k_scale,
+                           void* v_out, float* v_scale, void* k_mean,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Bytes of device workspace sage_attn_fwd needs for B x H heads of N tokens
  * of dimension D: per-batch (min doc, max doc, #valid, #padding) summaries of
  * every 64-key tile and 32- and 128-row query block (written and used when

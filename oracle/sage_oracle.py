@@ -71,6 +71,76 @@ def sm_scale_log2e(sm_scale: float) -> float:
 
 
 # ---------------------------------------------------------------------------
+# Producer of q, k, v: QKV split + per-head RMSNorm + Flux RoPE + transpose
+# (fused_qkv_postprocess, src/futudiffu/fused_kernels.py:271-390, op :613-643)
+# ---------------------------------------------------------------------------
+
+def sum_squares(x: torch.Tensor) -> torch.Tensor:
+    """fp64 sum of squares over the last dimension in the producer's fixed
+    order: each run of 8 channels left to right, then a pairwise tree over the
+    runs in channel order.  Returns ``[..., 1]``."""
+    d = x.shape[-1]
+    sq = (x.double() ** 2).unflatten(-1, (d // 8, 8))
+    runs = sq[..., 0]
+    for e in range(1, 8):
+        runs = runs + sq[..., e]
+    while runs.shape[-1] > 1:
+        runs = runs[..., 0::2] + runs[..., 1::2]
+    return runs
+
+
+def rms_rope(x: torch.Tensor, w: torch.Tensor, freqs: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm then rotary embedding of ``x`` (``[B, N, H, D]``, values of bf16),
+    returned in fp32 before the bf16 store.
+
+    fused_kernels.py:316-377: ``rrms = 1 / sqrt(mean(x^2) + eps)`` (:318-320),
+    ``n = x * rrms * w`` (:357-360), and per pair p of channels (2p, 2p+1) with
+    ``freqs[.., p] = [[cos, -sin], [sin, cos]]`` (:334-336):
+    ``even' = cos*n_even + (-sin)*n_odd``, ``odd' = sin*n_even + cos*n_odd``
+    (:363-366).  Definitions where the reference leaves the order open (as the
+    K mean in the module docstring): the sum of squares is taken in fp64 over
+    the bf16 squares in a fixed order -- each run of 8 channels left to right,
+    then a pairwise tree over the D/8 runs in channel order -- and rounded once
+    to fp32 with the division by D; every product and sum is a separately
+    rounded fp32 operation (no fused multiply-add).
+    """
+    d = x.shape[-1]
+    r32 = _round_f32
+    ms = r32(sum_squares(x) / d)
+    rrms = r32(1.0 / r32(torch.sqrt(r32(ms + float(_f32(eps))))))
+    n = r32(r32(x.double() * rrms) * w.float().double())
+    ne, no = n[..., 0::2], n[..., 1::2]
+    f = freqs.float().double()            # [B, N, 1, D/2, 2, 2], broadcast over heads
+    cos, nsin, sin = f[..., 0, 0], f[..., 0, 1], f[..., 1, 0]
+    re = r32(r32(cos * ne) + r32(nsin * no))
+    ro = r32(r32(sin * ne) + r32(cos * no))
+    return torch.stack([re, ro], dim=-1).flatten(-2).float()
+
+
+def _round_f32(t: torch.Tensor) -> torch.Tensor:
+    """Round fp64 values to the nearest fp32 (kept as fp64).  Applied to the
+    fp64 result of one +, -, *, / or sqrt of fp32 operands it gives exactly
+    the correctly rounded fp32 operation (fp64 carries more than 2*24+2 bits,
+    so the double rounding is innocuous), whatever the host's fp32 kernels do."""
+    return t.float().double()
+
+
+def qkv_postprocess(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, freqs: torch.Tensor,
+                    n_heads: int, head_dim: int, eps: float = 1e-5) -> tuple[torch.Tensor, ...]:
+    """bf16 ``q, k, v`` ``[B, H, N, D]`` from the QKV projection output ``[B, N, 3*H*D]``
+    (fused_kernels.py:271-390; torch form :517-541).  ``freqs`` is
+    ``[B, N, 1, D/2, 2, 2]`` fp32."""
+    b, n, _ = qkv.shape
+    x = qkv.view(b, n, 3, n_heads, head_dim)
+    if freqs.ndim == 5:
+        freqs = freqs.unsqueeze(2)
+    q = rms_rope(x[:, :, 0], q_norm_w, freqs, eps).to(torch.bfloat16)
+    k = rms_rope(x[:, :, 1], k_norm_w, freqs, eps).to(torch.bfloat16)
+    v = x[:, :, 2]
+    return tuple(t.movedim(1, 2).contiguous() for t in (q, k, v))
+
+
+# ---------------------------------------------------------------------------
 # K smoothing (sage_attention.py:63-71, called at :490-491)
 # ---------------------------------------------------------------------------
 

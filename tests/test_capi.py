@@ -118,6 +118,43 @@ def test_attn_rejects_bad_arguments(over, status, msg):
     assert msg in lib.sage_last_error().decode()
 
 
+def _prod_args(**over):
+    a = dict(qkv=16, qw=32, kw=48, fr=64, b=1, h=2, n=100, d=128, eps=1e-5)
+    a.update(over)
+    return [a[x] for x in ("qkv", "qw", "kw", "fr", "b", "h", "n", "d", "eps")]
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(b=0), 1, "positive"),
+    (dict(h=70000), 1, "grid limit"),
+    (dict(n=0), 1, "positive"),
+    (dict(d=96), 1, "head_dim"),
+    (dict(qkv=None), 1, "null"),
+    (dict(fr=None), 1, "null"),
+    (dict(qw=40), 2, "aligned"),
+    (dict(eps=-1.0), 1, "norm_eps"),
+])
+def test_producer_entries_reject_bad_arguments(over, status, msg):
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    assert lib.sage_qkv_postprocess(*_prod_args(**over), 80, 96, 112, None) == status
+    assert msg in lib.sage_last_error().decode()
+    assert lib.sage_quantize_from_qkv(*_prod_args(**over), 0, 1, 0, 1, 0.18, 128, 144, 160, 176, 192, 208, 224,
+                                      240, 1 << 20, None) == status
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_fused_quantize_entry_checks_outputs():
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    # v_scale missing for fp8 PV; workspace too small for smoothing
+    assert lib.sage_quantize_from_qkv(*_prod_args(), 0, 1, 0, 1, 0.18, 128, 144, 160, 176, 192, None, 224,
+                                      240, 1 << 20, None) == 1
+    assert "v_scale" in lib.sage_last_error().decode()
+    assert lib.sage_quantize_from_qkv(*_prod_args(), 0, 1, 0, 1, 0.18, 128, 144, 160, 176, 192, 208, 224,
+                                      240, 8, None) == 3
+
+
 def test_python_glue_error_types():
     from futudiffu_amd import sage_attention as SA
     q = torch.zeros(1, 2, 8, 64, dtype=torch.bfloat16)
@@ -157,6 +194,12 @@ def test_custom_op_schemas_and_fake_shapes():
         assert out.shape == (2, 40, 384) and lse.shape == (6, 40)
         out, lse = ops.sage_attn_ext(q, q, q, None, None, 0.1, "int8", "fp8", "token", True)
         assert out.shape == (2, 3, 40, 128)
+        # producer + attention from the QKV projection output
+        qkv = torch.empty(2, 40, 3 * 3 * 128, dtype=torch.bfloat16)
+        w = torch.empty(128)
+        fr = torch.empty(2, 40, 1, 64, 2, 2)
+        out, lse = ops.sage_attn_qkv_masked(qkv, w, w, fr, m, 3, 128, 1e-5, 0.1)
+        assert out.shape == (2, 40, 384) and lse.shape == (6, 40)
 
 
 def test_layout_round_trip():
