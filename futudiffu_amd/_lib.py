@@ -36,6 +36,10 @@ SIGNATURES = {
         _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_float, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_float,
         _P, _P, _P, _P, _P, _P, _P, _P, _c.c_size_t, _P]),
     "sage_doc_ids_from_cu_seqlens": (_c.c_int, [_P, _I64, _I64, _I64, _P, _P]),
+    "sage_attn_bwd_workspace_bytes": (_c.c_size_t, [_I64, _I64, _I64, _I64]),
+    "sage_attn_bwd": (_c.c_int, [
+        _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_float, _c.c_float,
+        _P, _I64, _I64, _I64, _P, _P, _c.c_size_t, _P, _P, _P, _P]),
 }
 
 _lock = threading.Lock()
@@ -56,7 +60,7 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
-            if lib.sage_abi_version() != 4:
+            if lib.sage_abi_version() != 5:
                 raise RuntimeError("libsage_mi355x.so ABI version mismatch")
             _lib = lib
         return _lib

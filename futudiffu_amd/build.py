@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libsage_mi355x.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["sage_quant.hip", "sage_attn.hip", "sage_mask.hip", "sage_capi.hip"]
+SOURCES = ["sage_quant.hip", "sage_attn.hip", "sage_mask.hip", "sage_bwd.hip", "sage_capi.hip"]
 ARCH = "gfx950"
 
 

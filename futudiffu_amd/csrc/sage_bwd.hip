@@ -1,0 +1,644 @@
+// Sage attention backward for gfx950 (CDNA4).
+//
+// Reference: the Triton kernels of sqcu/futudiffu src/futudiffu/sage_kernels.py:
+// the D pre-pass _sage_attn_d_prepass (:321-349), dK/dV
+// _sage_attn_bwd_dkdv_int8 (:805-916) and its tile-masked form (:1491-1615),
+// dQ _sage_attn_bwd_dq_int8 (:918-1030) and its tile-masked form (:1617-1722),
+// the fp8-QK kernels (:356-590); launchers sage_attention.py:344-458, :534-648.
+//
+// Operands.  P is recomputed from the forward's per-token codes exactly as the
+// forward scores them: s = (acc * qd) * kd (qd carrying sm_scale*log2(e)),
+// p = 2^(s - lse) with the forward's base-2 LSE.  The quantization kernel
+// supplies the Q and smoothed-K codes and scales and, given dO in place of V,
+// the T image of dO; timage_kernel writes the T images of Q and K~ and
+// delta_kernel D = rowsum(dO * O).
+//
+// T image of bf16 rows X [N, D]: per 64-token block, chunks (j, b, tt) of 64
+// lanes x 8 bf16, element 4jj + i of lane 32hh + r holding
+// X[32b + 16tt + 8jj + 4hh + i][32j + r].  It is the operand of
+// v_mfma_f32_32x32x16_bf16 for a contraction over tokens whose other operand
+// comes straight from a 32x32 accumulator (lane (h, r) holding rows
+// 8J + 4h + i, element 4J + i): lane half h supplies the same 8 tokens to both
+// operands.  The forward's bf16 V operand is the T image of V.
+//
+// dQ kernel: a workgroup is the forward's 128-query tile, 4 waves x 32
+// queries, streaming 64-key tiles through a two-stage LDS ring (registers
+// carry tile i+1 from global memory while tile i is consumed; one barrier per
+// tile).  Per wave and tile, in the S^T layout (lane (h, r) = query r, keys
+// 8J + 4h + i):
+//   S^T = K . Q^T (int8 / fp8 MFMA, the forward's operands),
+//   dP^T = V . dO^T (bf16 MFMA; V rows from LDS, the wave's dO rows in registers),
+//   dS^T = P^T (dP^T - D), dQ += dS . K~ (A = dS from the registers, B = T image of K~),
+// and dQ * sm_scale is rounded to bf16 at the end (sage_kernels.py:1720).
+// dK/dV kernel: a workgroup owns 128 keys, 32 per wave, and streams 64-query
+// steps.  Per wave and step, in the S layout (lane (h, r) = key r, queries
+// 8J + 4h + i):
+//   S = Q . K^T and dP = dO . V^T (the wave's K codes and V rows in registers),
+//   dS = P (dP - D), dV^T += dO^T . bf16(P), dK^T += Q^T . bf16(dS * sm_scale)
+// (A = the T images of dO and Q, B = P and dS from the registers).
+// Both kernels skip (query tile, key tile) pairs the reference tile mask turns
+// off; with document ids, hidden pairs get p = 0.
+#include "sage_common.h"
+#include "sage_launch.h"
+
+namespace sage {
+
+namespace {
+
+__device__ __forceinline__ uint32_t word_at(const uint4& w, int i) {
+  return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
+}
+
+__device__ __forceinline__ uint4 zero_if(bool z, uint4 w) { return z ? make_uint4(0, 0, 0, 0) : w; }
+
+// 16-byte staging unit as a native vector: copies are plain loads and stores,
+// so arrays of them stay in registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Slot (16-byte unit) of chunk ch of row `row` in an LDS tile of bf16 rows
+// whose chunks are XOR-swizzled by row, so that the 32 rows a fragment read
+// touches fall in distinct banks.
+template <int D>
+__device__ __forceinline__ int swz(int row, int ch) {
+  constexpr int CPR = D / 8;
+  return row * CPR + (ch ^ (row & (CPR - 1)));
+}
+
+template <int QK>
+struct BAcc {
+  using type = f32x16;
+};
+template <>
+struct BAcc<kQK_INT8> {
+  using type = i32x16;
+};
+
+// One 32x32 score block from code fragments: rows from `a` (A operand), columns
+// from `b`, contracting the D channels (chunks of 32).
+template <int D, int QK>
+__device__ __forceinline__ typename BAcc<QK>::type score_block(const i32x4* a, const i32x4* b) {
+  constexpr int NC = D / 32;
+  if constexpr (QK == kQK_INT8) {
+    i32x16 acc = i32x16{0};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[c], b[c], acc, 0, 0, 0);
+    return acc;
+  } else {
+    f32x16 acc = f32x16{0};
+#pragma unroll
+    for (int c = 0; c < NC; c += 2) {
+      const i32x8 aa = {a[c][0], a[c][1], a[c][2], a[c][3], a[c + 1][0], a[c + 1][1], a[c + 1][2], a[c + 1][3]};
+      const i32x8 bb = {b[c][0], b[c][1], b[c][2], b[c][3], b[c + 1][0], b[c + 1][1], b[c + 1][2], b[c + 1][3]};
+      acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aa, bb, acc, 0, 0, 0, 0, 0, 0);
+    }
+    return acc;
+  }
+}
+
+__device__ __forceinline__ bool doc_visible(int dq, int dk) { return dk >= 0 && (dq == dk || dq < 0); }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Preparation
+// ---------------------------------------------------------------------------
+
+// T images of up to two bf16 [BH, N, D] tensors (grid.z selects the job), rows
+// past N zero.  With mu set, the rows are bf16(x - mu) (the quantization's
+// smoothed K, sage_attention.py:63-71).  Grid (np / 64, BH, jobs).
+template <int D>
+__global__ void __launch_bounds__(256) timage_kernel(TImageJobs jobs, int64_t n, int64_t np) {
+  constexpr int LPR = D / 8;
+  constexpr int VTHREADS = 16 * LPR;  // 16 groups of 4 tokens
+  __shared__ __attribute__((aligned(16))) uint8_t img[2 * 64 * D];
+  const int z = blockIdx.z, bh = blockIdx.y, tid = threadIdx.x;
+  const int64_t tok0 = (int64_t)blockIdx.x * 64;
+  const uint16_t* x = jobs.x[z] + (int64_t)bh * n * D;
+  const uint16_t* mu = jobs.mu[z];
+  if (tid < VTHREADS) {
+    const int g = tid / LPR, c8 = tid % LPR;
+    uint4 w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t tok = tok0 + 4 * g + i;
+      w[i] = zero_if(tok >= n, *reinterpret_cast<const uint4*>(x + min(tok, n - 1) * D + c8 * 8));
+    }
+    float m8[8];
+    if (mu) {
+      const uint4 mw = *reinterpret_cast<const uint4*>(mu + (int64_t)bh * D + c8 * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m8[e] = bf16_to_f32((uint16_t)(word_at(mw, e >> 1) >> ((e & 1) * 16)));
+    }
+    const int b = g >> 3, tt = (g >> 2) & 1, jj = (g >> 1) & 1, hh = g & 1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = c8 * 8 + e, j = d >> 5, r = d & 31;
+      uint32_t t4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t u = (word_at(w[i], e >> 1) >> ((e & 1) * 16)) & 0xffffu;
+        if (mu && tok0 + 4 * g + i < n) u = f32_to_bf16_rne(bf16_to_f32((uint16_t)u) - m8[e]);
+        t4[i] = u;
+      }
+      uint2 pk;
+      pk.x = t4[0] | (t4[1] << 16);
+      pk.y = t4[2] | (t4[3] << 16);
+      *reinterpret_cast<uint2*>(img + (((((j * 2 + b) * 2 + tt) * 64 + 32 * hh + r) * 8) + 4 * jj) * 2) = pk;
+    }
+  }
+  __syncthreads();
+  uint4* o = reinterpret_cast<uint4*>(jobs.out[z] + ((int64_t)bh * np + tok0) * D);
+#pragma unroll
+  for (int i = tid; i < 64 * D * 2 / 16; i += 256) o[i] = reinterpret_cast<const uint4*>(img)[i];
+}
+
+// D = rowsum(dO * O) per token in fp32 (sage_kernels.py:321-349), zero past N.
+// Lane (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps; the products
+// are fp32, summed per lane then over the token's lanes.  Grid (np / 64, BH).
+template <int D>
+__global__ void __launch_bounds__(256) delta_kernel(const uint16_t* __restrict__ dout,
+                                                    const uint16_t* __restrict__ out, int64_t n, int64_t np,
+                                                    float* __restrict__ delta) {
+  constexpr int LPR = D / 8, RPP = 256 / LPR, PASSES = 64 / RPP;
+  const int bh = blockIdx.y, tid = threadIdx.x, c8 = tid % LPR, rr = tid / LPR;
+  const int64_t tok0 = (int64_t)blockIdx.x * 64;
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int64_t t = tok0 + rr + ps * RPP;
+    const int64_t row = ((int64_t)bh * n + min(t, n - 1)) * D + c8 * 8;
+    const uint4 a = *reinterpret_cast<const uint4*>(dout + row);
+    const uint4 o = *reinterpret_cast<const uint4*>(out + row);
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sh = (e & 1) * 16;
+      s += bf16_to_f32((uint16_t)(word_at(a, e >> 1) >> sh)) * bf16_to_f32((uint16_t)(word_at(o, e >> 1) >> sh));
+    }
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) s += __shfl_xor(s, off);
+    if (c8 == 0) delta[(int64_t)bh * np + t] = t < n ? s : 0.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ
+// ---------------------------------------------------------------------------
+
+// LDS stage of one 64-key tile: K codes (row fragments, as stored), V rows
+// (swizzled), the T image of K~, per-key K scales, per-key document ids.
+template <int D>
+struct DqStage {
+  static constexpr int kcBytes = 64 * D;
+  static constexpr int rowBytes = 64 * 2 * D;
+  static constexpr int offV = kcBytes;
+  static constexpr int offT = offV + rowBytes;
+  static constexpr int offKd = offT + rowBytes;
+  static constexpr int offDoc = offKd + 256;
+  static constexpr int bytes = offDoc + 256;
+  static constexpr int nKc = kcBytes / 16 / 256, nRow = rowBytes / 16 / 256;  // 16-byte chunks per thread
+};
+
+template <int D, int QK, int MASK>
+__global__ void __launch_bounds__(256, 1) bwd_dq_kernel(BwdParams p) {
+  using St = DqStage<D>;
+  using SAcc = typename BAcc<QK>::type;
+  constexpr int NC = D / 32, CPR = D / 8;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * St::bytes];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = lane >> 5, r = lane & 31;
+  const int bh = blockIdx.y, qt = blockIdx.x;
+  const int bidx = bh / p.h;
+  const int64_t n = p.n, np = p.np;
+  const int nt = (int)((n + 63) / 64);
+  const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * wave;
+  const bool wave_live = q0 < n;
+  const int64_t qrow = q0 + r;
+
+  // ---- per-wave query state -----------------------------------------------------
+  i32x4 qf[NC];
+  {
+    const uint8_t* qb = p.qc + ((int64_t)bh * np + q0) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qf[c] = *reinterpret_cast<const i32x4*>(qb + (c * 64 + lane) * 16);
+  }
+  bf16x8 dof[2 * NC];  // dO[qrow][16c2 + 8h, +8)
+  {
+    const uint16_t* dr = p.dout + ((int64_t)bh * n + min(qrow, n - 1)) * D + 8 * h;
+#pragma unroll
+    for (int c2 = 0; c2 < 2 * NC; ++c2) dof[c2] = *reinterpret_cast<const bf16x8*>(dr + 16 * c2);
+  }
+  const float qd = p.qs[(int64_t)bh * np + qrow];
+  const float lse_r = qrow < n ? p.lse[(int64_t)bh * n + qrow] : -INFINITY;
+  const bool row_live = lse_r > -INFINITY;
+  const float lse_b = row_live ? lse_r : 0.0f;
+  const float dl = p.delta[(int64_t)bh * np + qrow];
+  const int dq_doc = (MASK & 2) ? (qrow < n ? p.doc[(int64_t)bidx * n + qrow] : -1) : 0;
+  f32x16 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = f32x16{0};
+
+  auto active = [&](int t) __attribute__((always_inline)) -> bool {
+    if constexpr (MASK & 1) return p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] != 0;
+    return true;
+  };
+  auto next_active = [&](int t) __attribute__((always_inline)) -> int {
+    while (t < nt && !active(t)) ++t;
+    return t;
+  };
+
+  // ---- staging: global -> registers -> LDS -----------------------------------------
+  u32x4 pk[St::nKc], pv[St::nRow], pt[St::nRow], psm = u32x4{0, 0, 0, 0};
+  auto load_tile = [&](int t) __attribute__((always_inline)) {
+    const int64_t key0 = (int64_t)t * 64;
+    const u32x4* kcs = reinterpret_cast<const u32x4*>(p.kc + ((int64_t)bh * np + key0) * D);
+    const u32x4* tks = reinterpret_cast<const u32x4*>(p.tk + ((int64_t)bh * np + key0) * D);
+#pragma unroll
+    for (int i = 0; i < St::nKc; ++i) pk[i] = kcs[tid + 256 * i];
+#pragma unroll
+    for (int i = 0; i < St::nRow; ++i) {
+      const int x = tid + 256 * i, row = x / CPR, ch = x % CPR;
+      pv[i] = *reinterpret_cast<const u32x4*>(p.v + ((int64_t)bh * n + min(key0 + row, n - 1)) * D + ch * 8);
+      pt[i] = tks[x];
+    }
+    if (tid < 16) {
+      psm = reinterpret_cast<const u32x4*>(p.ks + (int64_t)bh * np + key0)[tid];
+    } else if ((MASK & 2) && tid < 32) {
+      const int64_t k = key0 + 4 * (tid - 16);
+      const int32_t* db = p.doc + (int64_t)bidx * n;
+      psm = u32x4{(uint32_t)(k + 0 < n ? db[k + 0] : -1), (uint32_t)(k + 1 < n ? db[k + 1] : -1),
+                  (uint32_t)(k + 2 < n ? db[k + 2] : -1), (uint32_t)(k + 3 < n ? db[k + 3] : -1)};
+    }
+  };
+  auto store_tile = [&](int stage) __attribute__((always_inline)) {
+    uint8_t* sb = smem + stage * St::bytes;
+#pragma unroll
+    for (int i = 0; i < St::nKc; ++i) reinterpret_cast<u32x4*>(sb)[tid + 256 * i] = pk[i];
+#pragma unroll
+    for (int i = 0; i < St::nRow; ++i) {
+      const int x = tid + 256 * i, row = x / CPR, ch = x % CPR;
+      reinterpret_cast<u32x4*>(sb + St::offV)[swz<D>(row, ch)] = pv[i];
+      reinterpret_cast<u32x4*>(sb + St::offT)[x] = pt[i];
+    }
+    if (tid < 16)
+      reinterpret_cast<u32x4*>(sb + St::offKd)[tid] = psm;
+    else if ((MASK & 2) && tid < 32)
+      reinterpret_cast<u32x4*>(sb + St::offDoc)[tid - 16] = psm;
+  };
+
+  int t = next_active(0);
+  if (t < nt) {
+    load_tile(t);
+    store_tile(0);
+  }
+  __syncthreads();
+  int stage = 0;
+  while (t < nt) {
+    const int tn = next_active(t + 1);
+    if (tn < nt) load_tile(tn);
+    if (wave_live) {
+      const uint8_t* sb = smem + stage * St::bytes;
+      // S^T = K . Q^T: rows = keys 32b + (lane-local rows), columns = this wave's queries
+      SAcc s[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        i32x4 ka[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) ka[c] = reinterpret_cast<const i32x4*>(sb)[(b * NC + c) * 64 + lane];
+        s[b] = score_block<D, QK>(ka, qf);
+      }
+      // dP^T = V . dO^T
+      f32x16 dp[2];
+      const u32x4* vl = reinterpret_cast<const u32x4*>(sb + St::offV);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        dp[b] = f32x16{0};
+#pragma unroll
+        for (int c2 = 0; c2 < 2 * NC; ++c2) {
+          const u32x4 w = vl[swz<D>(32 * b + r, 2 * c2 + h)];
+          dp[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), dof[c2], dp[b], 0, 0, 0);
+        }
+      }
+      // P^T, dS^T (bf16, packed as the A operand of dS . K~)
+      const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
+      const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
+      const int kmax = (int)min((int64_t)64, n - (int64_t)t * 64);  // valid keys of this tile
+      bf16x8 dsa[2][2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int J = 0; J < 4; ++J) {
+          const f32x4 kd4 = kdl[8 * b + 2 * J + h];
+          int4 dk4 = make_int4(0, 0, 0, 0);
+          if constexpr (MASK & 2) dk4 = dkl[8 * b + 2 * J + h];
+          const int dk[4] = {dk4.x, dk4.y, dk4.z, dk4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = 4 * J + i;
+            const int kloc = 32 * b + 8 * J + 4 * h + i;
+            bool vis = row_live && kloc < kmax;
+            if constexpr (MASK & 2) vis = vis && doc_visible(dq_doc, dk[i]);
+            const float sc = ((float)s[b][e] * qd) * kd4[i];
+            const float pr = vis ? __builtin_amdgcn_exp2f(sc - lse_b) : 0.0f;
+            const float ds = pr * (dp[b][e] - dl);
+            dsa[b][e >> 3][e & 7] = (__bf16)ds;
+          }
+        }
+      // dQ += dS . K~
+      const bf16x8* tkl = reinterpret_cast<const bf16x8*>(sb + St::offT);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+            acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(dsa[b][tt], tkl[((c * 2 + b) * 2 + tt) * 64 + lane],
+                                                             acc[c], 0, 0, 0);
+    }
+    if (tn < nt) store_tile(stage ^ 1);
+    __syncthreads();
+    stage ^= 1;
+    t = tn;
+  }
+
+  // ---- epilogue: dQ * sm_scale -> bf16, staged per wave as 32 rows, stored in rows ----
+  // acc lane (h, r) holds channel 32c + r of rows 8J + 4h + i (element 4J + i)
+  uint16_t* stg = reinterpret_cast<uint16_t*>(smem) + wave * 32 * D;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = 8 * (e >> 2) + 4 * h + (e & 3);
+      stg[row * D + 32 * c + r] = f32_to_bf16_rne(acc[c][e] * p.sm_scale);
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 32 * CPR / 64; ++i) {
+    const int x = lane + 64 * i, row = x / CPR, ch = x % CPR;
+    const int64_t q = q0 + row;
+    if (q < n)
+      *reinterpret_cast<uint4*>(p.dq + ((int64_t)bh * n + q) * D + ch * 8) =
+          reinterpret_cast<const uint4*>(stg)[x];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV
+// ---------------------------------------------------------------------------
+
+// LDS stage of one 64-query step: Q codes (row fragments), dO rows (swizzled),
+// T images of dO and Q, per-query Q scale, LSE (-inf past N), D, document ids.
+template <int D>
+struct DkvStage {
+  static constexpr int qcBytes = 64 * D;
+  static constexpr int rowBytes = 64 * 2 * D;
+  static constexpr int offDo = qcBytes;
+  static constexpr int offTdo = offDo + rowBytes;
+  static constexpr int offTq = offTdo + rowBytes;
+  static constexpr int offQd = offTq + rowBytes;
+  static constexpr int offLse = offQd + 256;
+  static constexpr int offDl = offLse + 256;
+  static constexpr int offDoc = offDl + 256;
+  static constexpr int bytes = offDoc + 256;
+  static constexpr int nQc = qcBytes / 16 / 256, nRow = rowBytes / 16 / 256;
+};
+
+template <int D, int QK, int MASK>
+__global__ void __launch_bounds__(256, 1) bwd_dkdv_kernel(BwdParams p) {
+  using St = DkvStage<D>;
+  using SAcc = typename BAcc<QK>::type;
+  constexpr int NC = D / 32, CPR = D / 8;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * St::bytes];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = lane >> 5, r = lane & 31;
+  const int bh = blockIdx.y, kb = blockIdx.x;
+  const int bidx = bh / p.h;
+  const int64_t n = p.n, np = p.np;
+  const int nkv = (int)((n + 63) / 64);
+  const int nsteps = (int)((n + 63) / 64);  // 64-query steps holding a query below N
+  const int64_t k0 = (int64_t)kb * kRowsPerWG + 32 * wave;
+  const int64_t krow = k0 + r;
+  const int my_tile = 2 * kb + (wave >> 1);  // reference KV tile of this wave's keys
+  const bool wave_live = k0 < n;
+
+  // ---- per-wave key state -------------------------------------------------------------
+  i32x4 kf[NC];
+  {
+    const uint8_t* kbp = p.kc + ((int64_t)bh * np + k0) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) kf[c] = *reinterpret_cast<const i32x4*>(kbp + (c * 64 + lane) * 16);
+  }
+  bf16x8 vf[2 * NC];  // V[krow][16c2 + 8h, +8)
+  {
+    const uint16_t* vr = p.v + ((int64_t)bh * n + min(krow, n - 1)) * D + 8 * h;
+#pragma unroll
+    for (int c2 = 0; c2 < 2 * NC; ++c2) vf[c2] = *reinterpret_cast<const bf16x8*>(vr + 16 * c2);
+  }
+  const float kd = p.ks[(int64_t)bh * np + krow];
+  const bool key_ok = krow < n;
+  const int dk_doc = (MASK & 2) ? (key_ok ? p.doc[(int64_t)bidx * n + krow] : -1) : 0;
+  f32x16 dva[NC], dka[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    dva[c] = f32x16{0};
+    dka[c] = f32x16{0};
+  }
+
+  const uint8_t* mrow = (MASK & 1) ? p.tile_mask + (int64_t)bh * p.mask_stride_z : nullptr;
+  auto wave_active = [&](int s) __attribute__((always_inline)) -> bool {
+    if constexpr (MASK & 1) return my_tile < nkv && mrow[(int64_t)(s >> 1) * p.mask_nkv + my_tile] != 0;
+    return true;
+  };
+  auto active = [&](int s) __attribute__((always_inline)) -> bool {
+    if constexpr (MASK & 1) {
+      const uint8_t* m = mrow + (int64_t)(s >> 1) * p.mask_nkv;
+      return m[2 * kb] != 0 || (2 * kb + 1 < nkv && m[2 * kb + 1] != 0);
+    }
+    return true;
+  };
+  auto next_active = [&](int s) __attribute__((always_inline)) -> int {
+    while (s < nsteps && !active(s)) ++s;
+    return s;
+  };
+
+  u32x4 pq[St::nQc], pd[St::nRow], ptd[St::nRow], ptq[St::nRow], psm = u32x4{0, 0, 0, 0};
+  auto load_step = [&](int s) __attribute__((always_inline)) {
+    const int64_t m0 = (int64_t)s * 64;
+    const u32x4* qcs = reinterpret_cast<const u32x4*>(p.qc + ((int64_t)bh * np + m0) * D);
+    const u32x4* tds = reinterpret_cast<const u32x4*>(p.tdo + ((int64_t)bh * np + m0) * D);
+    const u32x4* tqs = reinterpret_cast<const u32x4*>(p.tq + ((int64_t)bh * np + m0) * D);
+#pragma unroll
+    for (int i = 0; i < St::nQc; ++i) pq[i] = qcs[tid + 256 * i];
+#pragma unroll
+    for (int i = 0; i < St::nRow; ++i) {
+      const int x = tid + 256 * i, row = x / CPR, ch = x % CPR;
+      pd[i] = *reinterpret_cast<const u32x4*>(p.dout + ((int64_t)bh * n + min(m0 + row, n - 1)) * D + ch * 8);
+      ptd[i] = tds[x];
+      ptq[i] = tqs[x];
+    }
+    if (tid < 16) {
+      psm = reinterpret_cast<const u32x4*>(p.qs + (int64_t)bh * np + m0)[tid];
+    } else if (tid < 32) {
+      const int64_t m = m0 + 4 * (tid - 16);
+      const float* lb = p.lse + (int64_t)bh * n;
+      const uint32_t ninf = 0xff800000u;
+      psm = u32x4{m + 0 < n ? __float_as_uint(lb[m + 0]) : ninf, m + 1 < n ? __float_as_uint(lb[m + 1]) : ninf,
+                  m + 2 < n ? __float_as_uint(lb[m + 2]) : ninf, m + 3 < n ? __float_as_uint(lb[m + 3]) : ninf};
+    } else if (tid < 48) {
+      psm = reinterpret_cast<const u32x4*>(p.delta + (int64_t)bh * np + m0)[tid - 32];
+    } else if ((MASK & 2) && tid < 64) {
+      const int64_t m = m0 + 4 * (tid - 48);
+      const int32_t* db = p.doc + (int64_t)bidx * n;
+      psm = u32x4{(uint32_t)(m + 0 < n ? db[m + 0] : -1), (uint32_t)(m + 1 < n ? db[m + 1] : -1),
+                  (uint32_t)(m + 2 < n ? db[m + 2] : -1), (uint32_t)(m + 3 < n ? db[m + 3] : -1)};
+    }
+  };
+  auto store_step = [&](int stage) __attribute__((always_inline)) {
+    uint8_t* sb = smem + stage * St::bytes;
+#pragma unroll
+    for (int i = 0; i < St::nQc; ++i) reinterpret_cast<u32x4*>(sb)[tid + 256 * i] = pq[i];
+#pragma unroll
+    for (int i = 0; i < St::nRow; ++i) {
+      const int x = tid + 256 * i, row = x / CPR, ch = x % CPR;
+      reinterpret_cast<u32x4*>(sb + St::offDo)[swz<D>(row, ch)] = pd[i];
+      reinterpret_cast<u32x4*>(sb + St::offTdo)[x] = ptd[i];
+      reinterpret_cast<u32x4*>(sb + St::offTq)[x] = ptq[i];
+    }
+    if (tid < 48 || ((MASK & 2) && tid < 64)) reinterpret_cast<u32x4*>(sb + St::offQd)[tid] = psm;
+  };
+
+  int s = next_active(0);
+  if (s < nsteps) {
+    load_step(s);
+    store_step(0);
+  }
+  __syncthreads();
+  int stage = 0;
+  while (s < nsteps) {
+    const int sn = next_active(s + 1);
+    if (sn < nsteps) load_step(sn);
+    if (wave_live && wave_active(s)) {
+      const uint8_t* sb = smem + stage * St::bytes;
+      const f32x4* qdl = reinterpret_cast<const f32x4*>(sb + St::offQd);
+      const f32x4* lsl = reinterpret_cast<const f32x4*>(sb + St::offLse);
+      const f32x4* dll = reinterpret_cast<const f32x4*>(sb + St::offDl);
+      const int4* dql = reinterpret_cast<const int4*>(sb + St::offDoc);
+      const u32x4* dol = reinterpret_cast<const u32x4*>(sb + St::offDo);
+      const bf16x8* tdl = reinterpret_cast<const bf16x8*>(sb + St::offTdo);
+      const bf16x8* tql = reinterpret_cast<const bf16x8*>(sb + St::offTq);
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {  // 32-query halves of the step
+        // S = Q . K^T: rows = queries 32a + (lane-local rows), columns = this wave's keys
+        i32x4 qa[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) qa[c] = reinterpret_cast<const i32x4*>(sb)[(a * NC + c) * 64 + lane];
+        const SAcc sacc = score_block<D, QK>(qa, kf);
+        // dP = dO . V^T
+        f32x16 dp = f32x16{0};
+#pragma unroll
+        for (int c2 = 0; c2 < 2 * NC; ++c2) {
+          const u32x4 w = dol[swz<D>(32 * a + r, 2 * c2 + h)];
+          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), vf[c2], dp, 0, 0, 0);
+        }
+        bf16x8 pb[2], db[2];
+#pragma unroll
+        for (int J = 0; J < 4; ++J) {
+          const f32x4 qd4 = qdl[8 * a + 2 * J + h];
+          const f32x4 ls4 = lsl[8 * a + 2 * J + h];
+          const f32x4 dl4 = dll[8 * a + 2 * J + h];
+          int4 dq4 = make_int4(0, 0, 0, 0);
+          if constexpr (MASK & 2) dq4 = dql[8 * a + 2 * J + h];
+          const int dqd[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = 4 * J + i;
+            bool vis = key_ok && ls4[i] > -INFINITY;
+            if constexpr (MASK & 2) vis = vis && doc_visible(dqd[i], dk_doc);
+            const float sc = ((float)sacc[e] * qd4[i]) * kd;
+            const float pr = vis ? __builtin_amdgcn_exp2f(sc - ls4[i]) : 0.0f;
+            const float ds = pr * (dp[e] - dl4[i]);
+            pb[e >> 3][e & 7] = (__bf16)pr;
+            db[e >> 3][e & 7] = (__bf16)(ds * p.sm_scale);
+          }
+        }
+        // dV^T += dO^T . P, dK^T += Q^T . dS
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const int ci = ((c * 2 + a) * 2 + tt) * 64 + lane;
+            dva[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tdl[ci], pb[tt], dva[c], 0, 0, 0);
+            dka[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tql[ci], db[tt], dka[c], 0, 0, 0);
+          }
+      }
+    }
+    if (sn < nsteps) store_step(stage ^ 1);
+    __syncthreads();
+    stage ^= 1;
+    s = sn;
+  }
+
+  // ---- epilogue: lane (h, r) holds key r, channels 32c + 8J + 4h + i ----------------
+  if (key_ok) {
+    uint16_t* dvr = p.dv + ((int64_t)bh * n + krow) * D;
+    uint16_t* dkr = p.dk + ((int64_t)bh * n + krow) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        const int ch = 32 * c + 8 * J + 4 * h;
+        uint2 a, b;
+        a.x = f32_to_bf16_rne(dva[c][4 * J + 0]) | ((uint32_t)f32_to_bf16_rne(dva[c][4 * J + 1]) << 16);
+        a.y = f32_to_bf16_rne(dva[c][4 * J + 2]) | ((uint32_t)f32_to_bf16_rne(dva[c][4 * J + 3]) << 16);
+        b.x = f32_to_bf16_rne(dka[c][4 * J + 0]) | ((uint32_t)f32_to_bf16_rne(dka[c][4 * J + 1]) << 16);
+        b.y = f32_to_bf16_rne(dka[c][4 * J + 2]) | ((uint32_t)f32_to_bf16_rne(dka[c][4 * J + 3]) << 16);
+        *reinterpret_cast<uint2*>(dvr + ch) = a;
+        *reinterpret_cast<uint2*>(dkr + ch) = b;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+
+hipError_t launch_bwd_prep(const TImageJobs& jobs, int njobs, const uint16_t* dout, const uint16_t* out,
+                           int64_t bh, int64_t n, int64_t d, float* delta, hipStream_t st) {
+  const int64_t np = padded_len(n);
+  const dim3 gi((unsigned)(np / 64), (unsigned)bh, (unsigned)njobs), gd((unsigned)(np / 64), (unsigned)bh);
+  if (d == 128) {
+    if (njobs) hipLaunchKernelGGL(timage_kernel<128>, gi, dim3(256), 0, st, jobs, n, np);
+    hipLaunchKernelGGL(delta_kernel<128>, gd, dim3(256), 0, st, dout, out, n, np, delta);
+  } else if (d == 64) {
+    if (njobs) hipLaunchKernelGGL(timage_kernel<64>, gi, dim3(256), 0, st, jobs, n, np);
+    hipLaunchKernelGGL(delta_kernel<64>, gd, dim3(256), 0, st, dout, out, n, np, delta);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int D, int QK, int MASK>
+hipError_t launch_bwd_t(const BwdParams& p, int64_t bh, hipStream_t st) {
+  const dim3 grid((unsigned)(p.np / kRowsPerWG), (unsigned)bh);
+  hipLaunchKernelGGL((bwd_dkdv_kernel<D, QK, MASK>), grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((bwd_dq_kernel<D, QK, MASK>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_bwd_d(int qk, int mask, const BwdParams& p, int64_t bh, hipStream_t st) {
+#define SAGE_B_CASE(QK_, M_) \
+  if (qk == QK_ && mask == M_) return launch_bwd_t<D, QK_, M_>(p, bh, st);
+  SAGE_B_CASE(0, 0) SAGE_B_CASE(0, 1) SAGE_B_CASE(0, 2) SAGE_B_CASE(0, 3)
+  SAGE_B_CASE(1, 0) SAGE_B_CASE(1, 1) SAGE_B_CASE(1, 2) SAGE_B_CASE(1, 3)
+#undef SAGE_B_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_bwd(int qk, int mask, const BwdParams& p, int64_t d, int64_t bh, hipStream_t st) {
+  if (d == 128) return launch_bwd_d<128>(qk, mask, p, bh, st);
+  if (d == 64) return launch_bwd_d<64>(qk, mask, p, bh, st);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace sage

@@ -101,6 +101,35 @@ int check_producer(const void* qkv, const float* q_norm_w, const float* k_norm_w
   return SAGE_OK;
 }
 
+// Backward workspace: byte offsets of the quantization's outputs (codes,
+// scales, K mean, column-sum partials), the T images of dO, Q and K~, and D.
+struct BwdWorkspace {
+  size_t qc, qs, kc, ks, kmean, quant, tdo, tq, tk, delta, bytes;
+};
+
+BwdWorkspace bwd_workspace(int64_t bh, int64_t n, int64_t d) {
+  const size_t np = (size_t)sage::padded_len(n), rows = (size_t)bh * np;
+  BwdWorkspace w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = (off + bytes + 255) & ~(size_t)255;
+    return at;
+  };
+  w.qc = take(rows * d);
+  w.qs = take(rows * 4);
+  w.kc = take(rows * d);
+  w.ks = take(rows * 4);
+  w.kmean = take((size_t)bh * d * 2);
+  w.quant = take(sage::quant_workspace_bytes(bh, n, d));
+  w.tdo = take(rows * d * 2);
+  w.tq = take(rows * d * 2);
+  w.tk = take(rows * d * 2);
+  w.delta = take(rows * 4);
+  w.bytes = off;
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
@@ -244,6 +273,88 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(p.bh * nq));
   hipError_t e = sage::launch_attn(qk_kind, pv_kind, granularity, mask, p, d, (int)b, stream);
   return launch_status(e, "sage_attn_fwd");
+}
+
+size_t sage_attn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) {
+  return bwd_workspace(b * h, n, d).bytes;
+}
+
+int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, const float* lse, const void* dout,
+                  int64_t b, int64_t h, int64_t n, int64_t d, int qk_kind, int smooth_k, float sm_scale,
+                  float sm_scale_log2e, const uint8_t* tile_mask, int64_t mask_stride_z, int64_t mask_nq, int64_t mask_nkv,
+                  const int32_t* doc_ids, void* workspace, size_t workspace_bytes, void* dq, void* dk, void* dv,
+                  hipStream_t stream) {
+  if (b <= 0 || h <= 0) return fail(SAGE_ERR_ARG, "b=%lld and h=%lld must be positive", (long long)b, (long long)h);
+  int st = check_common(b * h, n, d, qk_kind, SAGE_PV_BF16, SAGE_GRAN_TOKEN);
+  if (st) return st;
+  if (!q || !k || !v || !out || !lse || !dout || !dq || !dk || !dv) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  const void* ptrs[] = {q, k, v, out, dout, dq, dk, dv};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
+  if (!(sm_scale > 0.0f) || !(sm_scale_log2e > 0.0f))
+    return fail(SAGE_ERR_ARG, "sm_scale and sm_scale_log2e must be positive");
+  const int64_t nq = (n + 127) / 128, nkv = (n + 63) / 64;
+  int mask = 0;
+  if (tile_mask) {
+    if (mask_nq != nq || mask_nkv != nkv)
+      return fail(SAGE_ERR_ARG, "block_mask must be %lld x %lld tiles, got %lld x %lld", (long long)nq,
+                  (long long)nkv, (long long)mask_nq, (long long)mask_nkv);
+    if (mask_stride_z != 0 && mask_stride_z != nq * nkv)
+      return fail(SAGE_ERR_ARG, "mask_stride_z must be 0 (2D mask) or %lld (3D mask)", (long long)(nq * nkv));
+    mask |= 1;
+  }
+  if (doc_ids) mask |= 2;
+  const BwdWorkspace ws = bwd_workspace(b * h, n, d);
+  if (!workspace || workspace_bytes < ws.bytes)
+    return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", ws.bytes, workspace_bytes);
+  if (!aligned16(workspace)) return fail(SAGE_ERR_ALIGN, "workspace must be 16-byte aligned");
+  uint8_t* w = static_cast<uint8_t*>(workspace);
+  const int64_t bh = b * h;
+  const auto* q16 = static_cast<const uint16_t*>(q);
+  const auto* k16 = static_cast<const uint16_t*>(k);
+  const auto* do16 = static_cast<const uint16_t*>(dout);
+  // codes, scales and the K mean of the forward's per-token quantization;
+  // dO takes the place of V, so the bf16 "V operand" written is dO's T image
+  hipError_t e = sage::launch_quantize(
+      qk_kind, SAGE_PV_BF16, SAGE_GRAN_TOKEN, smooth_k != 0, q16, k16, do16, bh, n, d,
+      sm_scale_log2e, reinterpret_cast<double*>(w + ws.quant), w + ws.qc,
+      reinterpret_cast<float*>(w + ws.qs), w + ws.kc, reinterpret_cast<float*>(w + ws.ks), w + ws.tdo, nullptr,
+      reinterpret_cast<uint16_t*>(w + ws.kmean), sage::ProdArgs{}, stream);
+  if (e != hipSuccess) return launch_status(e, "sage_attn_bwd (quantize)");
+  sage::TImageJobs jobs{};
+  jobs.x[0] = q16;
+  jobs.out[0] = reinterpret_cast<uint16_t*>(w + ws.tq);
+  jobs.x[1] = k16;
+  jobs.mu[1] = smooth_k ? reinterpret_cast<const uint16_t*>(w + ws.kmean) : nullptr;
+  jobs.out[1] = reinterpret_cast<uint16_t*>(w + ws.tk);
+  e = sage::launch_bwd_prep(jobs, 2, do16, static_cast<const uint16_t*>(out), bh, n, d,
+                            reinterpret_cast<float*>(w + ws.delta), stream);
+  if (e != hipSuccess) return launch_status(e, "sage_attn_bwd (prep)");
+  sage::BwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.qc = w + ws.qc;
+  p.qs = reinterpret_cast<const float*>(w + ws.qs);
+  p.kc = w + ws.kc;
+  p.ks = reinterpret_cast<const float*>(w + ws.ks);
+  p.v = static_cast<const uint16_t*>(v);
+  p.dout = do16;
+  p.tq = reinterpret_cast<const uint16_t*>(w + ws.tq);
+  p.tk = reinterpret_cast<const uint16_t*>(w + ws.tk);
+  p.tdo = reinterpret_cast<const uint16_t*>(w + ws.tdo);
+  p.lse = lse;
+  p.delta = reinterpret_cast<const float*>(w + ws.delta);
+  p.tile_mask = tile_mask;
+  p.mask_stride_z = mask_stride_z;
+  p.mask_nkv = mask_nkv;
+  p.doc = doc_ids;
+  p.dq = static_cast<uint16_t*>(dq);
+  p.dk = static_cast<uint16_t*>(dk);
+  p.dv = static_cast<uint16_t*>(dv);
+  p.n = n;
+  p.np = sage::padded_len(n);
+  p.h = (int)h;
+  p.sm_scale = sm_scale;
+  return launch_status(sage::launch_bwd(qk_kind, mask, p, d, bh, stream), "sage_attn_bwd");
 }
 
 int sage_build_tile_mask(const int32_t* doc_ids, int64_t b, int64_t n, int32_t pad_fill, uint8_t* mask,

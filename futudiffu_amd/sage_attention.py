@@ -1,4 +1,4 @@
-"""SageAttention forward on MI355X: host-side mirror of the reference API.
+"""SageAttention forward and backward on MI355X: host-side mirror of the reference API.
 
 Mirrors ``src/futudiffu/sage_attention.py`` of sqcu/futudiffu (function names,
 argument meaning and error behaviour) on top of the gfx950 HIP library
@@ -9,6 +9,8 @@ argument meaning and error behaviour) on top of the gfx950 HIP library
 * ``sage_attn_forward_masked``             -> :183-268
 * ``sage_attn_forward_with_lse``           -> :271-341
 * ``sage_attn_forward_masked_with_lse``    -> :461-531
+* ``sage_attn_backward``                   -> :344-458
+* ``sage_attn_backward_masked``            -> :534-648
 
 Each call runs two kernels on the current stream: ``sage_quantize_qkv``
 (K smoothing + Q/K/V quantization) and ``sage_attn_fwd``.  All outputs and
@@ -361,6 +363,65 @@ def sage_attn_forward_masked_merged_heads(q: Tensor, k: Tensor, v: Tensor, block
     """
     return sage_forward(q, k, v, sm_scale, block_mask=block_mask, doc_ids=doc_ids, qk=qk, pv=pv,
                         granularity=granularity, out_layout="bnhd")
+
+
+def sage_backward(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor, dout: Tensor,
+                  sm_scale: float | None = None, *, block_mask: Tensor | None = None,
+                  doc_ids: Tensor | None = None, qk: str | None = None,
+                  smooth_k: bool | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """dQ, dK, dV (bf16 ``[B, H, N, D]``) with explicit variant selection.
+
+    P is recomputed from per-token Q / K codes (K smoothed again when
+    ``smooth_k``) and the forward's base-2 ``lse``; ``smooth_k``, the mask and
+    ``doc_ids`` must be the forward's.  Runs the quantization, the T-image and
+    D pre-pass kernels, then the dK/dV and dQ kernels (sage_kernels.py:321-349,
+    :805-1030, :1491-1722) on the current stream.
+    """
+    B, H, N, D = _check_inputs(q, k, v)
+    qk = _SAGE_QK_QUANT if qk is None else qk
+    smooth_k = _SAGE_SMOOTH_K if smooth_k is None else smooth_k
+    if qk not in _QK:
+        raise ValueError(f"Unknown qk_quant: {qk!r}")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    dev = q.device
+    for name, t in (("out", out), ("dout", dout)):
+        if tuple(t.shape) != (B, H, N, D) or t.dtype != torch.bfloat16 or t.device != dev:
+            raise ValueError(f"{name} must be a bf16 [{B}, {H}, {N}, {D}] tensor on {dev}")
+    if tuple(lse.shape) != (B * H, N) or lse.dtype != torch.float32 or lse.device != dev:
+        raise ValueError(f"lse must be an fp32 [{B * H}, {N}] tensor on {dev}")
+    q, k, v, out, dout, lse = (t.contiguous() for t in (q, k, v, out, dout, lse))
+    lib = _lib.load()
+    BH = B * H
+    bm, stride_z, nq, nkv = _norm_mask(block_mask, BH, N, dev)
+    if doc_ids is not None:
+        if doc_ids.shape != (B, N):
+            raise ValueError(f"doc_ids must be [B, N] = [{B}, {N}], got {tuple(doc_ids.shape)}")
+        doc_ids = doc_ids.to(device=dev, dtype=torch.int32).contiguous()
+    wsb = int(lib.sage_attn_bwd_workspace_bytes(B, H, N, D))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    _lib.check(lib.sage_attn_bwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(), dout.data_ptr(),
+        B, H, N, D, _QK[qk], int(bool(smooth_k)), float(sm_scale), _fold(sm_scale), _ptr(bm), stride_z, nq, nkv,
+        _ptr(doc_ids), ws.data_ptr(), wsb, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream_handle(dev)))
+    return dq, dk, dv
+
+
+def sage_attn_backward(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor, dout: Tensor,
+                       sm_scale: float) -> tuple[Tensor, Tensor, Tensor]:
+    """Backward of the unmasked forward with the configured QK quantization
+    and smoothing (sage_attention.py:344-458: int8 kernels when qk_quant is
+    "int8", the fp8 kernels otherwise)."""
+    return sage_backward(q, k, v, out, lse, dout, sm_scale)
+
+
+def sage_attn_backward_masked(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor, dout: Tensor,
+                              block_mask: Tensor, sm_scale: float, *,
+                              doc_ids: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """Backward of the block-masked forward: int8 P recomputation whatever the
+    configured QK quantization, configured smoothing (sage_attention.py:534-648)."""
+    return sage_backward(q, k, v, out, lse, dout, sm_scale, block_mask=block_mask, doc_ids=doc_ids, qk="int8")
 
 
 def qk_int32(q_codes: Tensor, k_codes: Tensor, bh: int, n: int, d: int) -> Tensor:

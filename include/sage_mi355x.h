@@ -1,5 +1,5 @@
 /*
- * sage_mi355x.h -- C ABI of the MI355X (gfx950) SageAttention forward.
+ * sage_mi355x.h -- C ABI of the MI355X (gfx950) SageAttention forward and backward.
  *
  * Drop-in boundary for the attention op that sqcu/futudiffu registers as
  *   futudiffu_ii::sage_attn_masked(q, k, v, block_mask, sm_scale) -> (out, lse)
@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 4
+#define SAGE_ABI_VERSION 5
 
 enum sage_status {
   SAGE_OK = 0,
@@ -215,6 +215,46 @@ int sage_build_tile_mask(const int32_t* doc_ids, int64_t b, int64_t n,
 int sage_doc_ids_from_cu_seqlens(const int32_t* cu_seqlens, int64_t b,
                                  int64_t n_segments, int64_t n,
                                  int32_t* doc_ids, hipStream_t stream);
+
+/* Bytes of the workspace sage_attn_bwd needs for b*h heads of n tokens of
+ * dimension D: the per-token Q / smoothed-K codes, scales and K mean, the
+ * K column-sum partials, bf16 operand images of dO, Q and the smoothed K
+ * (the bf16 v_codes layout above), and D = rowsum(dO * O) (fp32 [BH, Np]).
+ * No reference counterpart (the Triton launcher allocates these with torch). */
+size_t sage_attn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
+
+/* Attention backward: dQ, dK, dV from the forward's inputs, output and LSE.
+ * Replaces sage_attn_backward_masked (sage_attention.py:534-648) and
+ * sage_attn_backward (:344-458): the D pre-pass (sage_kernels.py:321-349),
+ * the dK/dV kernel (:805-916, tile-masked :1491-1615) and the dQ kernel
+ * (:918-1030, tile-masked :1617-1722), int8 or fp8 QK (:356-590).  P is
+ * recomputed from per-token codes of Q and of K (smoothed again when
+ * smooth_k != 0, which must match the forward), p = 2^(s - lse):
+ *   dV = bf16(P)^T dO, dK = bf16(dS * sm_scale)^T Q, dQ = (bf16(dS) K~) * sm_scale,
+ *   dS = P (dO V^T - D), each output rounded once to bf16.
+ *   q, k, v, out,
+ *   dout, dq, dk, dv  bf16 [BH, N, D] contiguous (the [B, H, N, D] tensors).
+ *   lse               fp32 [BH, N] from sage_attn_fwd (rows at -inf get no
+ *                     gradient).
+ *   qk_kind           SAGE_QK_INT8 (the reference's production backward) or
+ *                     SAGE_QK_FP8 (its fp8 kernels, :356-590).
+ *   sm_scale,
+ *   sm_scale_log2e    the softmax scale and its product with log2(e), the
+ *                     latter formed in double and rounded once (as passed to
+ *                     sage_quantize_qkv).
+ *   tile_mask, doc_ids  as in sage_attn_fwd; use the forward's.
+ *   workspace         sage_attn_bwd_workspace_bytes(b, h, n, d) bytes,
+ *                     16-byte aligned; concurrent calls need separate ones. */
+int sage_attn_bwd(const void* q, const void* k, const void* v,
+                  const void* out, const float* lse, const void* dout,
+                  int64_t b, int64_t h, int64_t n, int64_t d,
+                  int qk_kind, int smooth_k, float sm_scale, float sm_scale_log2e,
+                  const uint8_t* tile_mask, int64_t mask_stride_z,
+                  int64_t mask_nq, int64_t mask_nkv,
+                  const int32_t* doc_ids,
+                  void* workspace, size_t workspace_bytes,
+                  void* dq, void* dk, void* dv,
+                  hipStream_t stream);
 
 /* Debug/parity: int32 QK^T accumulators of int8 codes through the same MFMA
  * fragments as sage_attn_fwd, s_out int32 [BH, Np, Np] (row = query).

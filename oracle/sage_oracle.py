@@ -1,4 +1,4 @@
-"""CPU oracle for the Sage attention forward path (TEST INFRASTRUCTURE ONLY).
+"""CPU oracle for the Sage attention path (TEST INFRASTRUCTURE ONLY).
 
 This module is the checker, never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
@@ -514,6 +514,95 @@ def sdpa_fp64(q, k, v, sm_scale=None, visible=None):
                           else ~visible[:, None], -math.inf)
     lse = torch.logsumexp(s, dim=-1) * LOG2E
     return torch.matmul(torch.softmax(s, dim=-1), v.double()), lse.view(b * h, n)
+
+
+# ---------------------------------------------------------------------------
+# Backward (sage_attention.py:344-458 unmasked, :534-648 masked;
+# sage_kernels.py:321-349 D pre-pass, :805-1030 (int8) and :1491-1722 (int8,
+# tile-masked) dK/dV and dQ, :356-590 (fp8))
+# ---------------------------------------------------------------------------
+
+def delta_prepass(dout: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """``D_i = sum_d dO_id * O_id`` in fp32 ``[BH, N]`` (sage_kernels.py:321-349).
+
+    The products are fp32; the sum is formed in fp64 and rounded once (the
+    reference's ``tl.sum`` order is unspecified, so the sum is tolerance-level).
+    """
+    bh = dout.shape[0] * dout.shape[1] if dout.ndim == 4 else dout.shape[0]
+    n, d = dout.shape[-2], dout.shape[-1]
+    prod = dout.reshape(bh, n, d).float() * out.reshape(bh, n, d).float()
+    return prod.double().sum(-1).float()
+
+
+def sage_backward(q, k, v, out, lse, dout, sm_scale=None, qk="int8", smooth=True,
+                  block_mask=None, doc_ids=None, head_chunk=4):
+    """dQ, dK, dV (bf16 ``[B, H, N, D]``) of the Sage attention backward.
+
+    Follows sage_attn_backward_masked (sage_attention.py:534-648) and the
+    unmasked sage_attn_backward (:344-458); kernel lines below are those of
+    the tile-masked int8 kernels in sage_kernels.py:
+      * K is smoothed again (sage_attention.py:376 / :574) and Q, K quantized
+        per token exactly as in the forward (:1564-1567 / :1655-1658; the fp8
+        kernels the same formulas with 448, :415-418), Q's scale carrying
+        ``sm_scale*log2(e)``.
+      * ``s = (acc*qd)*kd`` with keys past N at -inf (:1571-1572);
+        ``p = 2^(s - lse)`` from the forward's base-2 LSE (:1577); rows past N
+        give p = 0 (:1578).  Tile-masked (query tile, key tile) pairs are
+        skipped, so p = 0 there (:1553, :1679); ``doc_ids`` applies the exact
+        per-token visibility instead (p = 0 where hidden).
+      * ``D = rowsum(dO * O)`` (:321-349); ``dP = dO @ V^T`` (fp32 accumulation
+        of bf16 operands, :1588); ``dS = P * (dP - D)`` (:1591).
+      * ``dV = bf16(P)^T @ dO`` (:1595), ``dK = bf16(dS * sm_scale)^T @ Q``
+        (:1592, :1599, Q the raw bf16 input), ``dQ = (bf16(dS) @ K~) * sm_scale``
+        (:1717, :1720, K~ the smoothed bf16 K), each rounded once to bf16.
+    Products are evaluated in fp64 from the bf16-rounded operands (fp32 in the
+    kernels: the difference is accumulation order only).
+
+    A row whose LSE is -inf (nothing visible in the forward) gets p = 0; the
+    reference would produce NaN there, and its tile masks never make one.
+    """
+    b, h, n, d = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    qz = quantize_all(q, k, v, sm_scale, qk, "bf16", "token", smooth)
+    bh = b * h
+    qf = q.reshape(bh, n, d)
+    vf = v.reshape(bh, n, d)
+    dof = dout.reshape(bh, n, d)
+    delta = delta_prepass(dout, out)
+    sm = _f32(sm_scale)
+    dqs, dks, dvs = [], [], []
+    for h0 in range(0, bh, head_chunk):
+        sel = slice(h0, min(h0 + head_chunk, bh))
+        s = scores(qz, qk, "token", sel)
+        vis = None
+        if block_mask is not None:
+            vm = block_mask
+            if vm.ndim == 3:
+                vm = vm[sel]
+            vis = tile_mask_visibility(vm, s.shape[0], n)
+        if doc_ids is not None:
+            bidx = torch.arange(sel.start, sel.stop) // h
+            dv_ = doc_visibility(doc_ids.to(torch.int64))[bidx]
+            vis = dv_ if vis is None else (vis & dv_)
+        ls = lse[sel][:, :, None]
+        live = torch.isfinite(ls)
+        p = torch.exp2(s - torch.where(live, ls, torch.zeros(())))
+        p = torch.where(live, p, torch.zeros(()))
+        if vis is not None:
+            p = torch.where(vis, p, torch.zeros(()))
+        do_ = dof[sel]
+        dp = torch.matmul(do_.double(), vf[sel].double().transpose(1, 2)).float()
+        ds = p * (dp - delta[sel][:, :, None])
+        pb = p.to(torch.bfloat16).double()
+        dvs.append(torch.matmul(pb.transpose(1, 2), do_.double()).to(torch.bfloat16))
+        dsk = (ds * sm).to(torch.bfloat16).double()
+        dks.append(torch.matmul(dsk.transpose(1, 2), qf[sel].double()).to(torch.bfloat16))
+        dsq = ds.to(torch.bfloat16).double()
+        dq = torch.matmul(dsq, qz.k_smoothed[sel].double()).float() * sm
+        dqs.append(dq.to(torch.bfloat16))
+    shape = (b, h, n, d)
+    return torch.cat(dqs).view(shape), torch.cat(dks).view(shape), torch.cat(dvs).view(shape)
 
 
 def make_inputs(b, h, n, d, seed=0, k_offset_std=2.0):

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), f"{name} declared in the header but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes prototype"
-    assert lib.sage_abi_version() == 4
+    assert lib.sage_abi_version() == 5
 
 
 def test_sizes_and_padding():
