@@ -89,6 +89,11 @@ CASES = {
     # writing bf16 q, k, v followed by the quantization
     "dit1280x832_int8fp8_from_qkv": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="fp8", gran="token",
                                          producer=True),
+    # the backward of the 1280x832 shape (int8 P recomputation, smoothing),
+    # unmasked and with the packed batch's reference tile mask
+    "dit1280x832_bwd_int8": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="bf16", gran="token", bwd=True),
+    "packed_tilemask_bwd_int8": dict(B=1, H=30, N=6912, D=128, qk="int8", pv="bf16", gran="token",
+                                     segments=[1280, 1216, 4416], mask="tile", bwd=True),
 }
 PEAK_MIXED_TFLOPS = 2.0 / (1.0 / PEAK_8BIT_TFLOPS + 1.0 / PEAK_BF16_TFLOPS)  # fp8 QK + bf16 PV
 
@@ -269,6 +274,70 @@ def _cpu_case(c, q, k, v, block_mask, doc, flop, budget_s):
     }
 
 
+def backward_case(args, name, c):
+    """Time the backward (quantization + operand images + D pre-pass + dK/dV +
+    dQ) on the forward's output.  Algorithmic FLOP = 10 * (visible pairs) * D:
+    the S recomputation (int8 / fp8), dP, dV, dK and dQ (2 each, the last four
+    bf16); the MFMA bound prices the first at the 8-bit peak and the rest at
+    the bf16 peak."""
+    from futudiffu_amd import sage_attention as SA
+    dev = torch.device("cuda:0")
+    B, H, N, D = c["B"], c["H"], c["N"], c["D"]
+    q, k, v, bm, doc, flop_fwd, extra = _case_inputs(c, dev)
+    pairs_d = flop_fwd / 4.0
+    flop = 10.0 * pairs_d
+    bound_s = 2.0 * pairs_d / (PEAK_8BIT_TFLOPS * 1e12) + 8.0 * pairs_d / (PEAK_BF16_TFLOPS * 1e12)
+    sm = 1.0 / math.sqrt(D)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    bmd = None if bm is None else bm.to(dev)
+    g = torch.Generator(device="cpu").manual_seed(7)
+    dout = torch.randn(B, H, N, D, generator=g).bfloat16()
+    dod = dout.to(dev)
+    out, lse = SA.sage_forward(qd, kd, vd, sm, block_mask=bmd, qk=c["qk"], pv=c["pv"], smooth_k=True)
+
+    def step():
+        return SA.sage_backward(qd, kd, vd, out, lse, dod, sm, block_mask=bmd, qk=c["qk"], smooth_k=True)
+
+    for _ in range(max(args.warmup // 4, 10)):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    steps = max(args.steps // 4, 5)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    tf = flop / (ms * 1e-3) / 1e12
+    line = {
+        "case": name,
+        "config": {k2: v2 for k2, v2 in c.items()},
+        "bwd_ms": round(ms, 5),
+        "bwd_tflops": round(tf, 2),
+        "flop": flop,
+        "roofline": {"bound": "mfma", "unit": "ms", "bound_ms": round(bound_s * 1e3, 5),
+                     "frac": round(bound_s * 1e3 / ms, 4),
+                     "peaks": f"S at {PEAK_8BIT_TFLOPS} TFLOP/s, dP/dV/dK/dQ at {PEAK_BF16_TFLOPS} TFLOP/s"},
+    }
+    line.update({k2: v2 for k2, v2 in extra.items() if k2 != "flop_dense"})
+    if not args.no_cpu_baseline:
+        from oracle import sage_oracle as O
+        q1, k1, v1, d1 = q[:1, :1], k[:1, :1], v[:1, :1], dout[:1, :1]
+        bm1 = None if bm is None else bm
+        o1, l1, _ = O.sage_forward(q1, k1, v1, sm, c["qk"], "bf16", "token", True, bm1)
+        t0 = time.perf_counter()
+        O.sage_backward(q1, k1, v1, o1, l1, d1, sm, qk=c["qk"], smooth=True, block_mask=bm1, head_chunk=1)
+        per_head = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": round(flop / (B * H) / per_head / 1e12, 6), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle backward (torch CPU restatement) of one head (batch 0, head 0): "
+                      f"{per_head * 1e3:.1f} ms/head, throughput on that head's share of the FLOPs",
+            "cpu_model": _cpu_model()}
+    print(json.dumps(line), flush=True)
+
+
 def all_configs(args):
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from futudiffu_amd import sage_attention as SA
@@ -278,6 +347,9 @@ def all_configs(args):
         c = CASES[name]
         B, H, N, D = c["B"], c["H"], c["N"], c["D"]
         print(f"# case {name}", file=sys.stderr, flush=True)
+        if c.get("bwd"):
+            backward_case(args, name, c)
+            continue
         q, k, v, bm, doc, flop, extra = _case_inputs(c, dev)
         qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
         bmd = None if bm is None else bm.to(dev)

@@ -149,7 +149,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // token's D channels (fused_kernels.py:316-320; the sum of squares in fp64, in
 // a fixed order: each lane's 8 channels left to right, then a pairwise tree
 // over the token's lanes; rounded once to fp32), n = x * rrms * w (:357-360), and per channel
-// pair (2p, 2p+1) with fr[p] = (cos, -sin, sin, cos) (:334-336):
+// pair (2p, 2p+1) with fr[p] = (cos, -sin, sin) (:334-336):
 // even' = cos*n_even + (-sin)*n_odd, odd' = sin*n_even + cos*n_odd (:363-366),
 // every product and sum a separately rounded fp32 operation.
 template <int D>
