@@ -33,7 +33,8 @@
 // dK/dV kernel: a workgroup owns 128 keys, 32 per wave, and streams 64-query
 // steps.  Per wave and step, in the S layout (lane (h, r) = key r, queries
 // 8J + 4h + i):
-//   S = Q . K^T and dP = dO . V^T (the wave's K codes and V rows in registers),
+//   S = Q . K^T and dP = dO . V^T (the wave's K codes in registers, the
+//   workgroup's V rows in LDS for the whole launch),
 //   dS = P (dP - D), dV^T += dO^T . bf16(P), dK^T += Q^T . bf16(dS * sm_scale)
 // (A = the T images of dO and Q, B = P and dS from the registers).
 // Both kernels skip (query tile, key tile) pairs the reference tile mask turns
@@ -195,22 +196,50 @@ struct DqStage {
   static constexpr int offKd = offT + rowBytes;
   static constexpr int offDoc = offKd + 256;
   static constexpr int bytes = offDoc + 256;
-  static constexpr int nKc = kcBytes / 16 / 256, nRow = rowBytes / 16 / 256;  // 16-byte chunks per thread
+  static constexpr int cKc = kcBytes / 16, cRow = rowBytes / 16;  // 16-byte chunks
 };
 
+// Threads of the backward workgroups: 8 waves, two per SIMD, so one wave's
+// vector work overlaps the other's matrix and LDS work.
+constexpr int kBwdThreads = 512;
+
+// Copies a region of C 16-byte chunks into LDS with direct global -> LDS
+// loads (global_load_lds_dwordx4): wave w moves the 64-chunk blocks w, w + 8,
+// ...; lane l of block j lands at LDS chunk 64 j + l, and src(x) is the
+// global address of chunk x.  No registers hold the data on its way; the
+// caller waits for vmcnt(0) before the barrier that publishes the stage.
+template <int C, typename Src>
+__device__ __forceinline__ void dma_chunks(uint8_t* lds, int wave, int lane, Src src) {
+  static_assert(C % 64 == 0, "whole 64-chunk blocks");
+  constexpr int kWaves = kBwdThreads / 64;
+#pragma unroll
+  for (int j0 = 0; j0 < C / 64; j0 += kWaves) {
+    const int j = j0 + wave;
+    if (j < C / 64) __builtin_amdgcn_global_load_lds(src(j * 64 + lane), lds + j * 1024, 16, 0, 0);
+  }
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left free; gfx9 encoding).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+// dQ.  Wave w covers queries 32 * (w % 4) of the workgroup's 128-query tile
+// and key half w / 4 of every 64-key tile; the two key halves' partial dQ are
+// summed (half 0 + half 1) at the end.
 template <int D, int QK, int MASK>
-__global__ void __launch_bounds__(256, 1) bwd_dq_kernel(BwdParams p) {
+__global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
   using St = DqStage<D>;
   using SAcc = typename BAcc<QK>::type;
   constexpr int NC = D / 32, CPR = D / 8;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * St::bytes];
+  static_assert(4 * NC * 16 * 64 * 4 <= 2 * St::bytes, "partial dQ exchange must fit in the ring");
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, r = lane & 31;
+  const int qg = wave & 3, b = wave >> 2;  // query group, key half
   const int bh = blockIdx.y, qt = blockIdx.x;
   const int bidx = bh / p.h;
   const int64_t n = p.n, np = p.np;
   const int nt = (int)((n + 63) / 64);
-  const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * wave;
+  const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * qg;
   const bool wave_live = q0 < n;
   const int64_t qrow = q0 + r;
 
@@ -246,20 +275,21 @@ __global__ void __launch_bounds__(256, 1) bwd_dq_kernel(BwdParams p) {
     return t;
   };
 
-  // ---- staging: global -> registers -> LDS -----------------------------------------
-  u32x4 pk[St::nKc], pv[St::nRow], pt[St::nRow], psm = u32x4{0, 0, 0, 0};
-  auto load_tile = [&](int t) __attribute__((always_inline)) {
+  // ---- staging: bulk by direct global -> LDS loads, scales / ids through registers ----
+  u32x4 psm = u32x4{0, 0, 0, 0};
+  auto load_tile = [&](int t, int stage) __attribute__((always_inline)) {
     const int64_t key0 = (int64_t)t * 64;
-    const u32x4* kcs = reinterpret_cast<const u32x4*>(p.kc + ((int64_t)bh * np + key0) * D);
-    const u32x4* tks = reinterpret_cast<const u32x4*>(p.tk + ((int64_t)bh * np + key0) * D);
-#pragma unroll
-    for (int i = 0; i < St::nKc; ++i) pk[i] = kcs[tid + 256 * i];
-#pragma unroll
-    for (int i = 0; i < St::nRow; ++i) {
-      const int x = tid + 256 * i, row = x / CPR, ch = x % CPR;
-      pv[i] = *reinterpret_cast<const u32x4*>(p.v + ((int64_t)bh * n + min(key0 + row, n - 1)) * D + ch * 8);
-      pt[i] = tks[x];
-    }
+    uint8_t* sb = smem + stage * St::bytes;
+    const uint8_t* kcs = p.kc + ((int64_t)bh * np + key0) * D;
+    const uint8_t* tks = reinterpret_cast<const uint8_t*>(p.tk + ((int64_t)bh * np + key0) * D);
+    const uint16_t* vs = p.v + (int64_t)bh * n * D;
+    dma_chunks<St::cKc>(sb, wave, lane, [&](int x) { return kcs + x * 16; });
+    dma_chunks<St::cRow>(sb + St::offT, wave, lane, [&](int x) { return tks + x * 16; });
+    // V rows: LDS slot x holds chunk ch of row `row` with x = swz(row, ch)
+    dma_chunks<St::cRow>(sb + St::offV, wave, lane, [&](int x) {
+      const int row = x / CPR, ch = (x % CPR) ^ (row & (CPR - 1));
+      return vs + min(key0 + row, n - 1) * D + ch * 8;
+    });
     if (tid < 16) {
       psm = reinterpret_cast<const u32x4*>(p.ks + (int64_t)bh * np + key0)[tid];
     } else if ((MASK & 2) && tid < 32) {
@@ -269,16 +299,8 @@ __global__ void __launch_bounds__(256, 1) bwd_dq_kernel(BwdParams p) {
                   (uint32_t)(k + 2 < n ? db[k + 2] : -1), (uint32_t)(k + 3 < n ? db[k + 3] : -1)};
     }
   };
-  auto store_tile = [&](int stage) __attribute__((always_inline)) {
+  auto store_small = [&](int stage) __attribute__((always_inline)) {
     uint8_t* sb = smem + stage * St::bytes;
-#pragma unroll
-    for (int i = 0; i < St::nKc; ++i) reinterpret_cast<u32x4*>(sb)[tid + 256 * i] = pk[i];
-#pragma unroll
-    for (int i = 0; i < St::nRow; ++i) {
-      const int x = tid + 256 * i, row = x / CPR, ch = x % CPR;
-      reinterpret_cast<u32x4*>(sb + St::offV)[swz<D>(row, ch)] = pv[i];
-      reinterpret_cast<u32x4*>(sb + St::offT)[x] = pt[i];
-    }
     if (tid < 16)
       reinterpret_cast<u32x4*>(sb + St::offKd)[tid] = psm;
     else if ((MASK & 2) && tid < 32)
@@ -287,93 +309,101 @@ __global__ void __launch_bounds__(256, 1) bwd_dq_kernel(BwdParams p) {
 
   int t = next_active(0);
   if (t < nt) {
-    load_tile(t);
-    store_tile(0);
+    load_tile(t, 0);
+    store_small(0);
   }
+  wait_vmem();
   __syncthreads();
   int stage = 0;
   while (t < nt) {
     const int tn = next_active(t + 1);
-    if (tn < nt) load_tile(tn);
+    if (tn < nt) load_tile(tn, stage ^ 1);
     if (wave_live) {
       const uint8_t* sb = smem + stage * St::bytes;
-      // S^T = K . Q^T: rows = keys 32b + (lane-local rows), columns = this wave's queries
-      SAcc s[2];
+      // S^T = K . Q^T for keys 32b + (lane-local rows) x this wave's queries
+      i32x4 ka[NC];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        i32x4 ka[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) ka[c] = reinterpret_cast<const i32x4*>(sb)[(b * NC + c) * 64 + lane];
-        s[b] = score_block<D, QK>(ka, qf);
-      }
+      for (int c = 0; c < NC; ++c) ka[c] = reinterpret_cast<const i32x4*>(sb)[(b * NC + c) * 64 + lane];
+      const SAcc s = score_block<D, QK>(ka, qf);
       // dP^T = V . dO^T
-      f32x16 dp[2];
+      f32x16 dp = f32x16{0};
       const u32x4* vl = reinterpret_cast<const u32x4*>(sb + St::offV);
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        dp[b] = f32x16{0};
-#pragma unroll
-        for (int c2 = 0; c2 < 2 * NC; ++c2) {
-          const u32x4 w = vl[swz<D>(32 * b + r, 2 * c2 + h)];
-          dp[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), dof[c2], dp[b], 0, 0, 0);
-        }
+      for (int c2 = 0; c2 < 2 * NC; ++c2) {
+        const u32x4 w = vl[swz<D>(32 * b + r, 2 * c2 + h)];
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), dof[c2], dp, 0, 0, 0);
       }
       // P^T, dS^T (bf16, packed as the A operand of dS . K~)
       const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
       const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
       const int kmax = (int)min((int64_t)64, n - (int64_t)t * 64);  // valid keys of this tile
-      bf16x8 dsa[2][2];
+      bf16x8 dsa[2];
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int J = 0; J < 4; ++J) {
+        const f32x4 kd4 = kdl[8 * b + 2 * J + h];
+        int4 dk4 = make_int4(0, 0, 0, 0);
+        if constexpr (MASK & 2) dk4 = dkl[8 * b + 2 * J + h];
+        const int dk[4] = {dk4.x, dk4.y, dk4.z, dk4.w};
 #pragma unroll
-        for (int J = 0; J < 4; ++J) {
-          const f32x4 kd4 = kdl[8 * b + 2 * J + h];
-          int4 dk4 = make_int4(0, 0, 0, 0);
-          if constexpr (MASK & 2) dk4 = dkl[8 * b + 2 * J + h];
-          const int dk[4] = {dk4.x, dk4.y, dk4.z, dk4.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int e = 4 * J + i;
-            const int kloc = 32 * b + 8 * J + 4 * h + i;
-            bool vis = row_live && kloc < kmax;
-            if constexpr (MASK & 2) vis = vis && doc_visible(dq_doc, dk[i]);
-            const float sc = ((float)s[b][e] * qd) * kd4[i];
-            const float pr = vis ? __builtin_amdgcn_exp2f(sc - lse_b) : 0.0f;
-            const float ds = pr * (dp[b][e] - dl);
-            dsa[b][e >> 3][e & 7] = (__bf16)ds;
-          }
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * J + i;
+          const int kloc = 32 * b + 8 * J + 4 * h + i;
+          bool vis = row_live && kloc < kmax;
+          if constexpr (MASK & 2) vis = vis && doc_visible(dq_doc, dk[i]);
+          const float sc = ((float)s[e] * qd) * kd4[i];
+          const float pr = vis ? __builtin_amdgcn_exp2f(sc - lse_b) : 0.0f;
+          const float ds = pr * (dp[e] - dl);
+          dsa[e >> 3][e & 7] = (__bf16)ds;
         }
-      // dQ += dS . K~
+      }
+      // dQ += dS . K~ over this key half
       const bf16x8* tkl = reinterpret_cast<const bf16x8*>(sb + St::offT);
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-            acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(dsa[b][tt], tkl[((c * 2 + b) * 2 + tt) * 64 + lane],
-                                                             acc[c], 0, 0, 0);
+        for (int tt = 0; tt < 2; ++tt)
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(dsa[tt], tkl[((c * 2 + b) * 2 + tt) * 64 + lane], acc[c],
+                                                           0, 0, 0);
     }
-    if (tn < nt) store_tile(stage ^ 1);
+    if (tn < nt) store_small(stage ^ 1);
+    wait_vmem();
     __syncthreads();
     stage ^= 1;
     t = tn;
   }
 
-  // ---- epilogue: dQ * sm_scale -> bf16, staged per wave as 32 rows, stored in rows ----
+  // ---- epilogue: dQ = (half 0 + half 1) * sm_scale -> bf16 ---------------------------
   // acc lane (h, r) holds channel 32c + r of rows 8J + 4h + i (element 4J + i)
-  uint16_t* stg = reinterpret_cast<uint16_t*>(smem) + wave * 32 * D;
+  float* xch = reinterpret_cast<float*>(smem) + qg * NC * 16 * 64;
+  if (b == 1) {
 #pragma unroll
-  for (int c = 0; c < NC; ++c)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int row = 8 * (e >> 2) + 4 * h + (e & 3);
-      stg[row * D + 32 * c + r] = f32_to_bf16_rne(acc[c][e] * p.sm_scale);
-    }
+      for (int e = 0; e < 16; ++e) xch[(c * 16 + e) * 64 + lane] = acc[c][e];
+  }
   __syncthreads();
+  if (b == 0) {
 #pragma unroll
-  for (int i = 0; i < 32 * CPR / 64; ++i) {
-    const int x = lane + 64 * i, row = x / CPR, ch = x % CPR;
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[c][e] += xch[(c * 16 + e) * 64 + lane];
+  }
+  __syncthreads();
+  uint16_t* stg = reinterpret_cast<uint16_t*>(smem) + qg * 32 * D;
+  if (b == 0) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = 8 * (e >> 2) + 4 * h + (e & 3);
+        stg[row * D + 32 * c + r] = f32_to_bf16_rne(acc[c][e] * p.sm_scale);
+      }
+  }
+  __syncthreads();
+  // all 8 waves store: wave w writes half (w / 4) of the rows of query group w % 4
+#pragma unroll
+  for (int i = 0; i < 16 * CPR / 64; ++i) {
+    const int x = 16 * CPR * b + lane + 64 * i, row = x / CPR, ch = x % CPR;
     const int64_t q = q0 + row;
     if (q < n)
       *reinterpret_cast<uint4*>(p.dq + ((int64_t)bh * n + q) * D + ch * 8) =
@@ -399,25 +429,33 @@ struct DkvStage {
   static constexpr int offDl = offLse + 256;
   static constexpr int offDoc = offDl + 256;
   static constexpr int bytes = offDoc + 256;
-  static constexpr int nQc = qcBytes / 16 / 256, nRow = rowBytes / 16 / 256;
+  static constexpr int cQc = qcBytes / 16, cRow = rowBytes / 16;
 };
 
+// dK, dV.  Wave w owns keys 32 * (w % 4) of the workgroup's 128 keys and
+// query half w / 4 of every 64-query step; the two query halves' partial dK
+// and dV are summed (half 0 + half 1) at the end.
 template <int D, int QK, int MASK>
-__global__ void __launch_bounds__(256, 1) bwd_dkdv_kernel(BwdParams p) {
+__global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
   using St = DkvStage<D>;
   using SAcc = typename BAcc<QK>::type;
   constexpr int NC = D / 32, CPR = D / 8;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * St::bytes];
+  // two step stages, then the workgroup's 128 V rows (swizzled), read as the
+  // B operand of dP by the waves that own them
+  constexpr int kVOff = 2 * St::bytes;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kVOff + kRowsPerWG * 2 * D];
+  static_assert(4 * NC * 16 * 64 * 4 <= 2 * St::bytes, "partial dK/dV exchange must fit in the ring");
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, r = lane & 31;
+  const int kg = wave & 3, a = wave >> 2;  // key group, query half
   const int bh = blockIdx.y, kb = blockIdx.x;
   const int bidx = bh / p.h;
   const int64_t n = p.n, np = p.np;
   const int nkv = (int)((n + 63) / 64);
   const int nsteps = (int)((n + 63) / 64);  // 64-query steps holding a query below N
-  const int64_t k0 = (int64_t)kb * kRowsPerWG + 32 * wave;
+  const int64_t k0 = (int64_t)kb * kRowsPerWG + 32 * kg;
   const int64_t krow = k0 + r;
-  const int my_tile = 2 * kb + (wave >> 1);  // reference KV tile of this wave's keys
+  const int my_tile = 2 * kb + (kg >> 1);  // reference KV tile of this wave's keys
   const bool wave_live = k0 < n;
 
   // ---- per-wave key state -------------------------------------------------------------
@@ -427,12 +465,16 @@ __global__ void __launch_bounds__(256, 1) bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) kf[c] = *reinterpret_cast<const i32x4*>(kbp + (c * 64 + lane) * 16);
   }
-  bf16x8 vf[2 * NC];  // V[krow][16c2 + 8h, +8)
   {
-    const uint16_t* vr = p.v + ((int64_t)bh * n + min(krow, n - 1)) * D + 8 * h;
-#pragma unroll
-    for (int c2 = 0; c2 < 2 * NC; ++c2) vf[c2] = *reinterpret_cast<const bf16x8*>(vr + 16 * c2);
+    // V rows kb*128 + row (clamped below N) into the persistent region
+    const uint16_t* vs = p.v + (int64_t)bh * n * D;
+    const int64_t r0 = (int64_t)kb * kRowsPerWG;
+    dma_chunks<kRowsPerWG * CPR>(smem + kVOff, wave, lane, [&](int x) {
+      const int row = x / CPR, ch = (x % CPR) ^ (row & (CPR - 1));
+      return vs + min(r0 + row, n - 1) * D + ch * 8;
+    });
   }
+  const u32x4* vrl = reinterpret_cast<const u32x4*>(smem + kVOff);
   const float kd = p.ks[(int64_t)bh * np + krow];
   const bool key_ok = krow < n;
   const int dk_doc = (MASK & 2) ? (key_ok ? p.doc[(int64_t)bidx * n + krow] : -1) : 0;
@@ -460,21 +502,23 @@ __global__ void __launch_bounds__(256, 1) bwd_dkdv_kernel(BwdParams p) {
     return s;
   };
 
-  u32x4 pq[St::nQc], pd[St::nRow], ptd[St::nRow], ptq[St::nRow], psm = u32x4{0, 0, 0, 0};
-  auto load_step = [&](int s) __attribute__((always_inline)) {
+  // ---- staging: bulk by direct global -> LDS loads, per-query values through registers ----
+  u32x4 psm = u32x4{0, 0, 0, 0};
+  auto load_step = [&](int s, int stage) __attribute__((always_inline)) {
     const int64_t m0 = (int64_t)s * 64;
-    const u32x4* qcs = reinterpret_cast<const u32x4*>(p.qc + ((int64_t)bh * np + m0) * D);
-    const u32x4* tds = reinterpret_cast<const u32x4*>(p.tdo + ((int64_t)bh * np + m0) * D);
-    const u32x4* tqs = reinterpret_cast<const u32x4*>(p.tq + ((int64_t)bh * np + m0) * D);
-#pragma unroll
-    for (int i = 0; i < St::nQc; ++i) pq[i] = qcs[tid + 256 * i];
-#pragma unroll
-    for (int i = 0; i < St::nRow; ++i) {
-      const int x = tid + 256 * i, row = x / CPR, ch = x % CPR;
-      pd[i] = *reinterpret_cast<const u32x4*>(p.dout + ((int64_t)bh * n + min(m0 + row, n - 1)) * D + ch * 8);
-      ptd[i] = tds[x];
-      ptq[i] = tqs[x];
-    }
+    uint8_t* sb = smem + stage * St::bytes;
+    const uint8_t* qcs = p.qc + ((int64_t)bh * np + m0) * D;
+    const uint8_t* tds = reinterpret_cast<const uint8_t*>(p.tdo + ((int64_t)bh * np + m0) * D);
+    const uint8_t* tqs = reinterpret_cast<const uint8_t*>(p.tq + ((int64_t)bh * np + m0) * D);
+    const uint16_t* dos = p.dout + (int64_t)bh * n * D;
+    dma_chunks<St::cQc>(sb, wave, lane, [&](int x) { return qcs + x * 16; });
+    dma_chunks<St::cRow>(sb + St::offTdo, wave, lane, [&](int x) { return tds + x * 16; });
+    dma_chunks<St::cRow>(sb + St::offTq, wave, lane, [&](int x) { return tqs + x * 16; });
+    // dO rows: LDS slot x holds chunk ch of row `row` with x = swz(row, ch)
+    dma_chunks<St::cRow>(sb + St::offDo, wave, lane, [&](int x) {
+      const int row = x / CPR, ch = (x % CPR) ^ (row & (CPR - 1));
+      return dos + min(m0 + row, n - 1) * D + ch * 8;
+    });
     if (tid < 16) {
       psm = reinterpret_cast<const u32x4*>(p.qs + (int64_t)bh * np + m0)[tid];
     } else if (tid < 32) {
@@ -492,30 +536,22 @@ __global__ void __launch_bounds__(256, 1) bwd_dkdv_kernel(BwdParams p) {
                   (uint32_t)(m + 2 < n ? db[m + 2] : -1), (uint32_t)(m + 3 < n ? db[m + 3] : -1)};
     }
   };
-  auto store_step = [&](int stage) __attribute__((always_inline)) {
+  auto store_small = [&](int stage) __attribute__((always_inline)) {
     uint8_t* sb = smem + stage * St::bytes;
-#pragma unroll
-    for (int i = 0; i < St::nQc; ++i) reinterpret_cast<u32x4*>(sb)[tid + 256 * i] = pq[i];
-#pragma unroll
-    for (int i = 0; i < St::nRow; ++i) {
-      const int x = tid + 256 * i, row = x / CPR, ch = x % CPR;
-      reinterpret_cast<u32x4*>(sb + St::offDo)[swz<D>(row, ch)] = pd[i];
-      reinterpret_cast<u32x4*>(sb + St::offTdo)[x] = ptd[i];
-      reinterpret_cast<u32x4*>(sb + St::offTq)[x] = ptq[i];
-    }
     if (tid < 48 || ((MASK & 2) && tid < 64)) reinterpret_cast<u32x4*>(sb + St::offQd)[tid] = psm;
   };
 
   int s = next_active(0);
   if (s < nsteps) {
-    load_step(s);
-    store_step(0);
+    load_step(s, 0);
+    store_small(0);
   }
+  wait_vmem();
   __syncthreads();
   int stage = 0;
   while (s < nsteps) {
     const int sn = next_active(s + 1);
-    if (sn < nsteps) load_step(sn);
+    if (sn < nsteps) load_step(sn, stage ^ 1);
     if (wave_live && wave_active(s)) {
       const uint8_t* sb = smem + stage * St::bytes;
       const f32x4* qdl = reinterpret_cast<const f32x4*>(sb + St::offQd);
@@ -525,60 +561,82 @@ __global__ void __launch_bounds__(256, 1) bwd_dkdv_kernel(BwdParams p) {
       const u32x4* dol = reinterpret_cast<const u32x4*>(sb + St::offDo);
       const bf16x8* tdl = reinterpret_cast<const bf16x8*>(sb + St::offTdo);
       const bf16x8* tql = reinterpret_cast<const bf16x8*>(sb + St::offTq);
+      // S = Q . K^T: rows = queries 32a + (lane-local rows), columns = this wave's keys
+      i32x4 qa[NC];
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {  // 32-query halves of the step
-        // S = Q . K^T: rows = queries 32a + (lane-local rows), columns = this wave's keys
-        i32x4 qa[NC];
+      for (int c = 0; c < NC; ++c) qa[c] = reinterpret_cast<const i32x4*>(sb)[(a * NC + c) * 64 + lane];
+      const SAcc sacc = score_block<D, QK>(qa, kf);
+      // dP = dO . V^T
+      f32x16 dp = f32x16{0};
 #pragma unroll
-        for (int c = 0; c < NC; ++c) qa[c] = reinterpret_cast<const i32x4*>(sb)[(a * NC + c) * 64 + lane];
-        const SAcc sacc = score_block<D, QK>(qa, kf);
-        // dP = dO . V^T
-        f32x16 dp = f32x16{0};
-#pragma unroll
-        for (int c2 = 0; c2 < 2 * NC; ++c2) {
-          const u32x4 w = dol[swz<D>(32 * a + r, 2 * c2 + h)];
-          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), vf[c2], dp, 0, 0, 0);
-        }
-        bf16x8 pb[2], db[2];
-#pragma unroll
-        for (int J = 0; J < 4; ++J) {
-          const f32x4 qd4 = qdl[8 * a + 2 * J + h];
-          const f32x4 ls4 = lsl[8 * a + 2 * J + h];
-          const f32x4 dl4 = dll[8 * a + 2 * J + h];
-          int4 dq4 = make_int4(0, 0, 0, 0);
-          if constexpr (MASK & 2) dq4 = dql[8 * a + 2 * J + h];
-          const int dqd[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int e = 4 * J + i;
-            bool vis = key_ok && ls4[i] > -INFINITY;
-            if constexpr (MASK & 2) vis = vis && doc_visible(dqd[i], dk_doc);
-            const float sc = ((float)sacc[e] * qd4[i]) * kd;
-            const float pr = vis ? __builtin_amdgcn_exp2f(sc - ls4[i]) : 0.0f;
-            const float ds = pr * (dp[e] - dl4[i]);
-            pb[e >> 3][e & 7] = (__bf16)pr;
-            db[e >> 3][e & 7] = (__bf16)(ds * p.sm_scale);
-          }
-        }
-        // dV^T += dO^T . P, dK^T += Q^T . dS
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            const int ci = ((c * 2 + a) * 2 + tt) * 64 + lane;
-            dva[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tdl[ci], pb[tt], dva[c], 0, 0, 0);
-            dka[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tql[ci], db[tt], dka[c], 0, 0, 0);
-          }
+      for (int c2 = 0; c2 < 2 * NC; ++c2) {
+        const u32x4 w = dol[swz<D>(32 * a + r, 2 * c2 + h)];
+        const u32x4 vv = vrl[swz<D>(32 * kg + r, 2 * c2 + h)];  // V[krow][16c2 + 8h, +8)
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, vv),
+                                                     dp, 0, 0, 0);
       }
+      bf16x8 pb[2], db[2];
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        const f32x4 qd4 = qdl[8 * a + 2 * J + h];
+        const f32x4 ls4 = lsl[8 * a + 2 * J + h];
+        const f32x4 dl4 = dll[8 * a + 2 * J + h];
+        int4 dq4 = make_int4(0, 0, 0, 0);
+        if constexpr (MASK & 2) dq4 = dql[8 * a + 2 * J + h];
+        const int dqd[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * J + i;
+          bool vis = key_ok && ls4[i] > -INFINITY;
+          if constexpr (MASK & 2) vis = vis && doc_visible(dqd[i], dk_doc);
+          const float sc = ((float)sacc[e] * qd4[i]) * kd;
+          const float pr = vis ? __builtin_amdgcn_exp2f(sc - ls4[i]) : 0.0f;
+          const float ds = pr * (dp[e] - dl4[i]);
+          pb[e >> 3][e & 7] = (__bf16)pr;
+          db[e >> 3][e & 7] = (__bf16)(ds * p.sm_scale);
+        }
+      }
+      // dV^T += dO^T . P, dK^T += Q^T . dS over this query half
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int ci = ((c * 2 + a) * 2 + tt) * 64 + lane;
+          dva[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tdl[ci], pb[tt], dva[c], 0, 0, 0);
+          dka[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tql[ci], db[tt], dka[c], 0, 0, 0);
+        }
     }
-    if (sn < nsteps) store_step(stage ^ 1);
+    if (sn < nsteps) store_small(stage ^ 1);
+    wait_vmem();
     __syncthreads();
     stage ^= 1;
     s = sn;
   }
 
-  // ---- epilogue: lane (h, r) holds key r, channels 32c + 8J + 4h + i ----------------
-  if (key_ok) {
+  // ---- epilogue: (half 0 + half 1), lane (h, r) holds key r, channels 32c + 8J + 4h + i ----
+  float* xch = reinterpret_cast<float*>(smem) + kg * NC * 16 * 64;
+  if (a == 1) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xch[(c * 16 + e) * 64 + lane] = dva[c][e];
+  }
+  __syncthreads();
+  if (a == 0) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dva[c][e] += xch[(c * 16 + e) * 64 + lane];
+  }
+  __syncthreads();
+  if (a == 1) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xch[(c * 16 + e) * 64 + lane] = dka[c][e];
+  }
+  __syncthreads();
+  if (a == 0 && key_ok) {
     uint16_t* dvr = p.dv + ((int64_t)bh * n + krow) * D;
     uint16_t* dkr = p.dk + ((int64_t)bh * n + krow) * D;
 #pragma unroll
@@ -586,13 +644,16 @@ __global__ void __launch_bounds__(256, 1) bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
       for (int J = 0; J < 4; ++J) {
         const int ch = 32 * c + 8 * J + 4 * h;
-        uint2 a, b;
-        a.x = f32_to_bf16_rne(dva[c][4 * J + 0]) | ((uint32_t)f32_to_bf16_rne(dva[c][4 * J + 1]) << 16);
-        a.y = f32_to_bf16_rne(dva[c][4 * J + 2]) | ((uint32_t)f32_to_bf16_rne(dva[c][4 * J + 3]) << 16);
-        b.x = f32_to_bf16_rne(dka[c][4 * J + 0]) | ((uint32_t)f32_to_bf16_rne(dka[c][4 * J + 1]) << 16);
-        b.y = f32_to_bf16_rne(dka[c][4 * J + 2]) | ((uint32_t)f32_to_bf16_rne(dka[c][4 * J + 3]) << 16);
-        *reinterpret_cast<uint2*>(dvr + ch) = a;
-        *reinterpret_cast<uint2*>(dkr + ch) = b;
+        float kk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kk[i] = dka[c][4 * J + i] + xch[(c * 16 + 4 * J + i) * 64 + lane];
+        uint2 va, ka2;
+        va.x = f32_to_bf16_rne(dva[c][4 * J + 0]) | ((uint32_t)f32_to_bf16_rne(dva[c][4 * J + 1]) << 16);
+        va.y = f32_to_bf16_rne(dva[c][4 * J + 2]) | ((uint32_t)f32_to_bf16_rne(dva[c][4 * J + 3]) << 16);
+        ka2.x = f32_to_bf16_rne(kk[0]) | ((uint32_t)f32_to_bf16_rne(kk[1]) << 16);
+        ka2.y = f32_to_bf16_rne(kk[2]) | ((uint32_t)f32_to_bf16_rne(kk[3]) << 16);
+        *reinterpret_cast<uint2*>(dvr + ch) = va;
+        *reinterpret_cast<uint2*>(dkr + ch) = ka2;
       }
   }
 }
@@ -620,8 +681,8 @@ hipError_t launch_bwd_prep(const TImageJobs& jobs, int njobs, const uint16_t* do
 template <int D, int QK, int MASK>
 hipError_t launch_bwd_t(const BwdParams& p, int64_t bh, hipStream_t st) {
   const dim3 grid((unsigned)(p.np / kRowsPerWG), (unsigned)bh);
-  hipLaunchKernelGGL((bwd_dkdv_kernel<D, QK, MASK>), grid, dim3(256), 0, st, p);
-  hipLaunchKernelGGL((bwd_dq_kernel<D, QK, MASK>), grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((bwd_dkdv_kernel<D, QK, MASK>), grid, dim3(kBwdThreads), 0, st, p);
+  hipLaunchKernelGGL((bwd_dq_kernel<D, QK, MASK>), grid, dim3(kBwdThreads), 0, st, p);
   return hipGetLastError();
 }
 
