@@ -39,6 +39,8 @@
 // (A = the T images of dO and Q, B = P and dS from the registers).
 // Both kernels skip (query tile, key tile) pairs the reference tile mask turns
 // off; with document ids, hidden pairs get p = 0.
+#include <type_traits>
+
 #include "sage_common.h"
 #include "sage_launch.h"
 
@@ -55,15 +57,6 @@ __device__ __forceinline__ uint4 zero_if(bool z, uint4 w) { return z ? make_uint
 // 16-byte staging unit as a native vector: copies are plain loads and stores,
 // so arrays of them stay in registers.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Slot (16-byte unit) of chunk ch of row `row` in an LDS tile of bf16 rows
-// whose chunks are XOR-swizzled by row, so that the 32 rows a fragment read
-// touches fall in distinct banks.
-template <int D>
-__device__ __forceinline__ int swz(int row, int ch) {
-  constexpr int CPR = D / 8;
-  return row * CPR + (ch ^ (row & (CPR - 1)));
-}
 
 template <int QK>
 struct BAcc {
@@ -153,6 +146,40 @@ __global__ void __launch_bounds__(256) timage_kernel(TImageJobs jobs, int64_t n,
   for (int i = tid; i < 64 * D * 2 / 16; i += 256) o[i] = reinterpret_cast<const uint4*>(img)[i];
 }
 
+// R images of up to two bf16 [BH, N, D] tensors (grid.z selects the job): per
+// 32-token block rb, 16-channel group c2 and lane L = 32h + r, the 16 bytes
+// X[32 rb + r][16 c2 + 8h, +8) at chunk (rb * D/16 + c2) * 64 + L, rows past N
+// zero.  It is the row operand of v_mfma_f32_32x32x16_bf16 contracting the
+// channels (lane (h, r) = row r, channels 8h.. of the 16-channel step), so a
+// stage is a contiguous copy and a fragment read is one 16-byte load per lane.
+// Grid (np / 64, BH, jobs), one thread per chunk.
+template <int D>
+__global__ void __launch_bounds__(256) rimage_kernel(TImageJobs jobs, int64_t n, int64_t np) {
+  constexpr int G = D / 16;           // 16-channel groups
+  constexpr int kChunks = 64 * D / 8;  // 16-byte chunks of a 64-token block
+  const int z = blockIdx.z, bh = blockIdx.y;
+  const int64_t tok0 = (int64_t)blockIdx.x * 64;
+  const uint16_t* x = jobs.x[z] + (int64_t)bh * n * D;
+  uint4* o = reinterpret_cast<uint4*>(jobs.out[z] + ((int64_t)bh * np + tok0) * D);
+#pragma unroll
+  for (int c = threadIdx.x; c < kChunks; c += 256) {
+    const int lane = c & 63, g = (c >> 6) % G, rb = (c >> 6) / G;
+    const int64_t row = tok0 + 32 * rb + (lane & 31);
+    const uint4 w = *reinterpret_cast<const uint4*>(x + min(row, n - 1) * D + 16 * g + 8 * (lane >> 5));
+    o[c] = zero_if(row >= n, w);
+  }
+}
+
+// Item of workgroup b of a 1D grid of `total` items: the hardware hands
+// workgroup b to XCD b % 8, and each XCD has its own L2, so every XCD takes a
+// contiguous range of items (head-major order) and its resident workgroups
+// share one head's operands.
+__device__ __forceinline__ int xcd_item(int b, int total) {
+  constexpr int kXcd = 8;
+  const int x = b % kXcd, local = b / kXcd, per = total / kXcd, rem = total % kXcd;
+  return x * per + min(x, rem) + local;
+}
+
 // D = rowsum(dO * O) per token in fp32 (sage_kernels.py:321-349), zero past N.
 // Lane (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps; the products
 // are fp32, summed per lane then over the token's lanes.  Grid (np / 64, BH).
@@ -185,8 +212,8 @@ __global__ void __launch_bounds__(256) delta_kernel(const uint16_t* __restrict__
 // dQ
 // ---------------------------------------------------------------------------
 
-// LDS stage of one 64-key tile: K codes (row fragments, as stored), V rows
-// (swizzled), the T image of K~, per-key K scales, per-key document ids.
+// LDS stage of one 64-key tile: K codes (row fragments, as stored), the R
+// image of V, the T image of K~, per-key K scales, per-key document ids.
 template <int D>
 struct DqStage {
   static constexpr int kcBytes = 64 * D;
@@ -235,7 +262,9 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, r = lane & 31;
   const int qg = wave & 3, b = wave >> 2;  // query group, key half
-  const int bh = blockIdx.y, qt = blockIdx.x;
+  const int nq = (int)(p.np / kRowsPerWG);
+  const int item = xcd_item(blockIdx.x, (int)gridDim.x);
+  const int bh = item / nq, qt = item % nq;
   const int bidx = bh / p.h;
   const int64_t n = p.n, np = p.np;
   const int nt = (int)((n + 63) / 64);
@@ -257,9 +286,10 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
     for (int c2 = 0; c2 < 2 * NC; ++c2) dof[c2] = *reinterpret_cast<const bf16x8*>(dr + 16 * c2);
   }
   const float qd = p.qs[(int64_t)bh * np + qrow];
+  // +inf for rows with no gradient (past N, or no visible key in the forward):
+  // 2^(s - inf) = 0 needs no per-element test
   const float lse_r = qrow < n ? p.lse[(int64_t)bh * n + qrow] : -INFINITY;
-  const bool row_live = lse_r > -INFINITY;
-  const float lse_b = row_live ? lse_r : 0.0f;
+  const float lse_b = lse_r > -INFINITY ? lse_r : INFINITY;
   const float dl = p.delta[(int64_t)bh * np + qrow];
   const int dq_doc = (MASK & 2) ? (qrow < n ? p.doc[(int64_t)bidx * n + qrow] : -1) : 0;
   f32x16 acc[NC];
@@ -282,14 +312,10 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
     uint8_t* sb = smem + stage * St::bytes;
     const uint8_t* kcs = p.kc + ((int64_t)bh * np + key0) * D;
     const uint8_t* tks = reinterpret_cast<const uint8_t*>(p.tk + ((int64_t)bh * np + key0) * D);
-    const uint16_t* vs = p.v + (int64_t)bh * n * D;
+    const uint8_t* rvs = reinterpret_cast<const uint8_t*>(p.rv + ((int64_t)bh * np + key0) * D);
     dma_chunks<St::cKc>(sb, wave, lane, [&](int x) { return kcs + x * 16; });
     dma_chunks<St::cRow>(sb + St::offT, wave, lane, [&](int x) { return tks + x * 16; });
-    // V rows: LDS slot x holds chunk ch of row `row` with x = swz(row, ch)
-    dma_chunks<St::cRow>(sb + St::offV, wave, lane, [&](int x) {
-      const int row = x / CPR, ch = (x % CPR) ^ (row & (CPR - 1));
-      return vs + min(key0 + row, n - 1) * D + ch * 8;
-    });
+    dma_chunks<St::cRow>(sb + St::offV, wave, lane, [&](int x) { return rvs + x * 16; });
     if (tid < 16) {
       psm = reinterpret_cast<const u32x4*>(p.ks + (int64_t)bh * np + key0)[tid];
     } else if ((MASK & 2) && tid < 32) {
@@ -330,7 +356,7 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
       const u32x4* vl = reinterpret_cast<const u32x4*>(sb + St::offV);
 #pragma unroll
       for (int c2 = 0; c2 < 2 * NC; ++c2) {
-        const u32x4 w = vl[swz<D>(32 * b + r, 2 * c2 + h)];
+        const u32x4 w = vl[(b * 2 * NC + c2) * 64 + lane];  // V[key 32b + r][16c2 + 8h, +8)
         dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), dof[c2], dp, 0, 0, 0);
       }
       // P^T, dS^T (bf16, packed as the A operand of dS . K~)
@@ -338,24 +364,29 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
       const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
       const int kmax = (int)min((int64_t)64, n - (int64_t)t * 64);  // valid keys of this tile
       bf16x8 dsa[2];
+      // s - lse = acc * (qd * kd) - lse; keys past N (the last tile only) are
+      // hidden by a test taken on that tile alone
+      auto scores = [&](auto ragged) __attribute__((always_inline)) {
 #pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        const f32x4 kd4 = kdl[8 * b + 2 * J + h];
-        int4 dk4 = make_int4(0, 0, 0, 0);
-        if constexpr (MASK & 2) dk4 = dkl[8 * b + 2 * J + h];
-        const int dk[4] = {dk4.x, dk4.y, dk4.z, dk4.w};
+        for (int J = 0; J < 4; ++J) {
+          const f32x4 kd4 = kdl[8 * b + 2 * J + h];
+          int4 dk4 = make_int4(0, 0, 0, 0);
+          if constexpr (MASK & 2) dk4 = dkl[8 * b + 2 * J + h];
+          const int dk[4] = {dk4.x, dk4.y, dk4.z, dk4.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int e = 4 * J + i;
-          const int kloc = 32 * b + 8 * J + 4 * h + i;
-          bool vis = row_live && kloc < kmax;
-          if constexpr (MASK & 2) vis = vis && doc_visible(dq_doc, dk[i]);
-          const float sc = ((float)s[e] * qd) * kd4[i];
-          const float pr = vis ? __builtin_amdgcn_exp2f(sc - lse_b) : 0.0f;
-          const float ds = pr * (dp[e] - dl);
-          dsa[e >> 3][e & 7] = (__bf16)ds;
+          for (int i = 0; i < 4; ++i) {
+            const int e = 4 * J + i;
+            float pr = __builtin_amdgcn_exp2f(fmaf((float)s[e], qd * kd4[i], -lse_b));
+            if constexpr (decltype(ragged)::value) pr = 32 * b + 8 * J + 4 * h + i < kmax ? pr : 0.0f;
+            if constexpr (MASK & 2) pr = doc_visible(dq_doc, dk[i]) ? pr : 0.0f;
+            dsa[e >> 3][e & 7] = (__bf16)(pr * (dp[e] - dl));
+          }
         }
-      }
+      };
+      if (kmax < 64)
+        scores(std::true_type{});
+      else
+        scores(std::false_type{});
       // dQ += dS . K~ over this key half
       const bf16x8* tkl = reinterpret_cast<const bf16x8*>(sb + St::offT);
 #pragma unroll
@@ -415,8 +446,9 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
 // dK, dV
 // ---------------------------------------------------------------------------
 
-// LDS stage of one 64-query step: Q codes (row fragments), dO rows (swizzled),
-// T images of dO and Q, per-query Q scale, LSE (-inf past N), D, document ids.
+// LDS stage of one 64-query step: Q codes (row fragments), the R image of dO,
+// T images of dO and Q, per-query Q scale, LSE (+inf for rows without
+// gradient), D, document ids.
 template <int D>
 struct DkvStage {
   static constexpr int qcBytes = 64 * D;
@@ -448,7 +480,9 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, r = lane & 31;
   const int kg = wave & 3, a = wave >> 2;  // key group, query half
-  const int bh = blockIdx.y, kb = blockIdx.x;
+  const int nkb = (int)(p.np / kRowsPerWG);
+  const int item = xcd_item(blockIdx.x, (int)gridDim.x);
+  const int bh = item / nkb, kb = item % nkb;
   const int bidx = bh / p.h;
   const int64_t n = p.n, np = p.np;
   const int nkv = (int)((n + 63) / 64);
@@ -466,13 +500,9 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
     for (int c = 0; c < NC; ++c) kf[c] = *reinterpret_cast<const i32x4*>(kbp + (c * 64 + lane) * 16);
   }
   {
-    // V rows kb*128 + row (clamped below N) into the persistent region
-    const uint16_t* vs = p.v + (int64_t)bh * n * D;
-    const int64_t r0 = (int64_t)kb * kRowsPerWG;
-    dma_chunks<kRowsPerWG * CPR>(smem + kVOff, wave, lane, [&](int x) {
-      const int row = x / CPR, ch = (x % CPR) ^ (row & (CPR - 1));
-      return vs + min(r0 + row, n - 1) * D + ch * 8;
-    });
+    // the R image of V rows [kb*128, +128) into the persistent region
+    const uint8_t* rvs = reinterpret_cast<const uint8_t*>(p.rv + ((int64_t)bh * np + (int64_t)kb * kRowsPerWG) * D);
+    dma_chunks<kRowsPerWG * CPR>(smem + kVOff, wave, lane, [&](int x) { return rvs + x * 16; });
   }
   const u32x4* vrl = reinterpret_cast<const u32x4*>(smem + kVOff);
   const float kd = p.ks[(int64_t)bh * np + krow];
@@ -510,23 +540,25 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
     const uint8_t* qcs = p.qc + ((int64_t)bh * np + m0) * D;
     const uint8_t* tds = reinterpret_cast<const uint8_t*>(p.tdo + ((int64_t)bh * np + m0) * D);
     const uint8_t* tqs = reinterpret_cast<const uint8_t*>(p.tq + ((int64_t)bh * np + m0) * D);
-    const uint16_t* dos = p.dout + (int64_t)bh * n * D;
+    const uint8_t* rds = reinterpret_cast<const uint8_t*>(p.rdo + ((int64_t)bh * np + m0) * D);
     dma_chunks<St::cQc>(sb, wave, lane, [&](int x) { return qcs + x * 16; });
     dma_chunks<St::cRow>(sb + St::offTdo, wave, lane, [&](int x) { return tds + x * 16; });
     dma_chunks<St::cRow>(sb + St::offTq, wave, lane, [&](int x) { return tqs + x * 16; });
-    // dO rows: LDS slot x holds chunk ch of row `row` with x = swz(row, ch)
-    dma_chunks<St::cRow>(sb + St::offDo, wave, lane, [&](int x) {
-      const int row = x / CPR, ch = (x % CPR) ^ (row & (CPR - 1));
-      return dos + min(m0 + row, n - 1) * D + ch * 8;
-    });
+    dma_chunks<St::cRow>(sb + St::offDo, wave, lane, [&](int x) { return rds + x * 16; });
     if (tid < 16) {
       psm = reinterpret_cast<const u32x4*>(p.qs + (int64_t)bh * np + m0)[tid];
     } else if (tid < 32) {
+      // the LSE, +inf for rows with no gradient (past N, or no visible key in
+      // the forward): 2^(s - inf) = 0 needs no per-element test
       const int64_t m = m0 + 4 * (tid - 16);
       const float* lb = p.lse + (int64_t)bh * n;
-      const uint32_t ninf = 0xff800000u;
-      psm = u32x4{m + 0 < n ? __float_as_uint(lb[m + 0]) : ninf, m + 1 < n ? __float_as_uint(lb[m + 1]) : ninf,
-                  m + 2 < n ? __float_as_uint(lb[m + 2]) : ninf, m + 3 < n ? __float_as_uint(lb[m + 3]) : ninf};
+      float l4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float l = m + i < n ? lb[m + i] : -INFINITY;
+        l4[i] = l > -INFINITY ? l : INFINITY;
+      }
+      psm = u32x4{__float_as_uint(l4[0]), __float_as_uint(l4[1]), __float_as_uint(l4[2]), __float_as_uint(l4[3])};
     } else if (tid < 48) {
       psm = reinterpret_cast<const u32x4*>(p.delta + (int64_t)bh * np + m0)[tid - 32];
     } else if ((MASK & 2) && tid < 64) {
@@ -570,8 +602,8 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
       f32x16 dp = f32x16{0};
 #pragma unroll
       for (int c2 = 0; c2 < 2 * NC; ++c2) {
-        const u32x4 w = dol[swz<D>(32 * a + r, 2 * c2 + h)];
-        const u32x4 vv = vrl[swz<D>(32 * kg + r, 2 * c2 + h)];  // V[krow][16c2 + 8h, +8)
+        const u32x4 w = dol[(a * 2 * NC + c2) * 64 + lane];    // dO[query 32a + r][16c2 + 8h, +8)
+        const u32x4 vv = vrl[(kg * 2 * NC + c2) * 64 + lane];  // V[krow][16c2 + 8h, +8)
         dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, vv),
                                                      dp, 0, 0, 0);
       }
@@ -584,13 +616,13 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
         int4 dq4 = make_int4(0, 0, 0, 0);
         if constexpr (MASK & 2) dq4 = dql[8 * a + 2 * J + h];
         const int dqd[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
+        // s - lse = acc * (qd * kd) - lse; keys past N need no test: their
+        // column only feeds their own dK / dV rows, which are not stored
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * J + i;
-          bool vis = key_ok && ls4[i] > -INFINITY;
-          if constexpr (MASK & 2) vis = vis && doc_visible(dqd[i], dk_doc);
-          const float sc = ((float)sacc[e] * qd4[i]) * kd;
-          const float pr = vis ? __builtin_amdgcn_exp2f(sc - ls4[i]) : 0.0f;
+          float pr = __builtin_amdgcn_exp2f(fmaf((float)sacc[e], qd4[i] * kd, -ls4[i]));
+          if constexpr (MASK & 2) pr = doc_visible(dqd[i], dk_doc) ? pr : 0.0f;
           const float ds = pr * (dp[e] - dl4[i]);
           pb[e >> 3][e & 7] = (__bf16)pr;
           db[e >> 3][e & 7] = (__bf16)(ds * p.sm_scale);
@@ -662,15 +694,17 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
 // Launchers
 // ---------------------------------------------------------------------------
 
-hipError_t launch_bwd_prep(const TImageJobs& jobs, int njobs, const uint16_t* dout, const uint16_t* out,
-                           int64_t bh, int64_t n, int64_t d, float* delta, hipStream_t st) {
+hipError_t launch_bwd_prep(const TImageJobs& tjobs, const TImageJobs& rjobs, const uint16_t* dout,
+                           const uint16_t* out, int64_t bh, int64_t n, int64_t d, float* delta, hipStream_t st) {
   const int64_t np = padded_len(n);
-  const dim3 gi((unsigned)(np / 64), (unsigned)bh, (unsigned)njobs), gd((unsigned)(np / 64), (unsigned)bh);
+  const dim3 g2((unsigned)(np / 64), (unsigned)bh, 2u), gd((unsigned)(np / 64), (unsigned)bh);
   if (d == 128) {
-    if (njobs) hipLaunchKernelGGL(timage_kernel<128>, gi, dim3(256), 0, st, jobs, n, np);
+    hipLaunchKernelGGL(timage_kernel<128>, g2, dim3(256), 0, st, tjobs, n, np);
+    hipLaunchKernelGGL(rimage_kernel<128>, g2, dim3(256), 0, st, rjobs, n, np);
     hipLaunchKernelGGL(delta_kernel<128>, gd, dim3(256), 0, st, dout, out, n, np, delta);
   } else if (d == 64) {
-    if (njobs) hipLaunchKernelGGL(timage_kernel<64>, gi, dim3(256), 0, st, jobs, n, np);
+    hipLaunchKernelGGL(timage_kernel<64>, g2, dim3(256), 0, st, tjobs, n, np);
+    hipLaunchKernelGGL(rimage_kernel<64>, g2, dim3(256), 0, st, rjobs, n, np);
     hipLaunchKernelGGL(delta_kernel<64>, gd, dim3(256), 0, st, dout, out, n, np, delta);
   } else {
     return hipErrorInvalidValue;
@@ -680,7 +714,7 @@ hipError_t launch_bwd_prep(const TImageJobs& jobs, int njobs, const uint16_t* do
 
 template <int D, int QK, int MASK>
 hipError_t launch_bwd_t(const BwdParams& p, int64_t bh, hipStream_t st) {
-  const dim3 grid((unsigned)(p.np / kRowsPerWG), (unsigned)bh);
+  const dim3 grid((unsigned)(p.np / kRowsPerWG * bh));  // items in xcd_item order
   hipLaunchKernelGGL((bwd_dkdv_kernel<D, QK, MASK>), grid, dim3(kBwdThreads), 0, st, p);
   hipLaunchKernelGGL((bwd_dq_kernel<D, QK, MASK>), grid, dim3(kBwdThreads), 0, st, p);
   return hipGetLastError();

@@ -104,7 +104,7 @@ int check_producer(const void* qkv, const float* q_norm_w, const float* k_norm_w
 // Backward workspace: byte offsets of the quantization's outputs (codes,
 // scales, K mean, column-sum partials), the T images of dO, Q and K~, and D.
 struct BwdWorkspace {
-  size_t qc, qs, kc, ks, kmean, quant, tdo, tq, tk, delta, bytes;
+  size_t qc, qs, kc, ks, kmean, quant, tdo, tq, tk, rdo, rv, delta, bytes;
 };
 
 BwdWorkspace bwd_workspace(int64_t bh, int64_t n, int64_t d) {
@@ -125,6 +125,8 @@ BwdWorkspace bwd_workspace(int64_t bh, int64_t n, int64_t d) {
   w.tdo = take(rows * d * 2);
   w.tq = take(rows * d * 2);
   w.tk = take(rows * d * 2);
+  w.rdo = take(rows * d * 2);
+  w.rv = take(rows * d * 2);
   w.delta = take(rows * 4);
   w.bytes = off;
   return w;
@@ -304,6 +306,8 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
     mask |= 1;
   }
   if (doc_ids) mask |= 2;
+  if ((b * h) * ((n + 127) / 128) > 0x7fffffff)
+    return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(b * h * ((n + 127) / 128)));
   const BwdWorkspace ws = bwd_workspace(b * h, n, d);
   if (!workspace || workspace_bytes < ws.bytes)
     return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", ws.bytes, workspace_bytes);
@@ -327,7 +331,12 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
   jobs.x[1] = k16;
   jobs.mu[1] = smooth_k ? reinterpret_cast<const uint16_t*>(w + ws.kmean) : nullptr;
   jobs.out[1] = reinterpret_cast<uint16_t*>(w + ws.tk);
-  e = sage::launch_bwd_prep(jobs, 2, do16, static_cast<const uint16_t*>(out), bh, n, d,
+  sage::TImageJobs rjobs{};
+  rjobs.x[0] = do16;
+  rjobs.out[0] = reinterpret_cast<uint16_t*>(w + ws.rdo);
+  rjobs.x[1] = static_cast<const uint16_t*>(v);
+  rjobs.out[1] = reinterpret_cast<uint16_t*>(w + ws.rv);
+  e = sage::launch_bwd_prep(jobs, rjobs, do16, static_cast<const uint16_t*>(out), bh, n, d,
                             reinterpret_cast<float*>(w + ws.delta), stream);
   if (e != hipSuccess) return launch_status(e, "sage_attn_bwd (prep)");
   sage::BwdParams p;
@@ -341,6 +350,8 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
   p.tq = reinterpret_cast<const uint16_t*>(w + ws.tq);
   p.tk = reinterpret_cast<const uint16_t*>(w + ws.tk);
   p.tdo = reinterpret_cast<const uint16_t*>(w + ws.tdo);
+  p.rdo = reinterpret_cast<const uint16_t*>(w + ws.rdo);
+  p.rv = reinterpret_cast<const uint16_t*>(w + ws.rv);
   p.lse = lse;
   p.delta = reinterpret_cast<const float*>(w + ws.delta);
   p.tile_mask = tile_mask;

@@ -115,8 +115,8 @@ hipError_t launch_tile_mask(const int32_t* doc, int64_t nb, int64_t n, int32_t p
 // Backward (sage_kernels.py:321-349, :805-1030, :1491-1722).  Codes and
 // scales are the quantization's per-token outputs ([BH, Np] layout, Q scale
 // with sm_scale*log2(e)); tq / tk / tdo are T images [BH, Np, D] of Q, the
-// smoothed K and dO; v, dout, lse and the gradients are unpadded [BH, N(, D)];
-// delta is [BH, Np].
+// smoothed K and dO, rdo / rv R images of dO and V; v, dout, lse and the
+// gradients are unpadded [BH, N(, D)]; delta is [BH, Np].
 struct BwdParams {
   const uint8_t* qc;
   const float* qs;
@@ -127,6 +127,8 @@ struct BwdParams {
   const uint16_t* tq;
   const uint16_t* tk;
   const uint16_t* tdo;
+  const uint16_t* rdo;  // R images [BH, Np, D] of dO and V
+  const uint16_t* rv;
   const float* lse;
   const float* delta;
   const uint8_t* tile_mask;
@@ -141,16 +143,16 @@ struct BwdParams {
   float sm_scale;
 };
 
-// Up to two T-image jobs of one launch: x [BH, N, D] bf16 -> out [BH, Np, D],
-// with mu ([BH, D] bf16) subtracted when set.
+// Two operand-image jobs of one launch: x [BH, N, D] bf16 -> out [BH, Np, D]
+// (T or R image), with mu ([BH, D] bf16) subtracted when set (T images only).
 struct TImageJobs {
   const uint16_t* x[2];
   const uint16_t* mu[2];
   uint16_t* out[2];
 };
 
-hipError_t launch_bwd_prep(const TImageJobs& jobs, int njobs, const uint16_t* dout, const uint16_t* out,
-                           int64_t bh, int64_t n, int64_t d, float* delta, hipStream_t st);
+hipError_t launch_bwd_prep(const TImageJobs& tjobs, const TImageJobs& rjobs, const uint16_t* dout,
+                           const uint16_t* out, int64_t bh, int64_t n, int64_t d, float* delta, hipStream_t st);
 hipError_t launch_bwd(int qk, int mask, const BwdParams& p, int64_t d, int64_t bh, hipStream_t st);
 hipError_t launch_doc_from_cu(const int32_t* cu, int64_t nb, int64_t nseg, int64_t n, int32_t* doc,
                               hipStream_t st);
