@@ -230,24 +230,11 @@ struct DqStage {
 // vector work overlaps the other's matrix and LDS work.
 constexpr int kBwdThreads = 512;
 
-// Copies a region of C 16-byte chunks into LDS with direct global -> LDS
-// loads (global_load_lds_dwordx4): wave w moves the 64-chunk blocks w, w + 8,
-// ...; lane l of block j lands at LDS chunk 64 j + l, and src(x) is the
-// global address of chunk x.  No registers hold the data on its way; the
-// caller waits for vmcnt(0) before the barrier that publishes the stage.
+// Direct global -> LDS copies by the 8 waves of a backward workgroup.
 template <int C, typename Src>
 __device__ __forceinline__ void dma_chunks(uint8_t* lds, int wave, int lane, Src src) {
-  static_assert(C % 64 == 0, "whole 64-chunk blocks");
-  constexpr int kWaves = kBwdThreads / 64;
-#pragma unroll
-  for (int j0 = 0; j0 < C / 64; j0 += kWaves) {
-    const int j = j0 + wave;
-    if (j < C / 64) __builtin_amdgcn_global_load_lds(src(j * 64 + lane), lds + j * 1024, 16, 0, 0);
-  }
+  sage::dma_chunks<C, kBwdThreads / 64>(lds, wave, lane, src);
 }
-
-// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left free; gfx9 encoding).
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 // dQ.  Wave w covers queries 32 * (w % 4) of the workgroup's 128-query tile
 // and key half w / 4 of every 64-key tile; the two key halves' partial dQ are

@@ -56,6 +56,26 @@ __device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d
   return x0 | (x1 << 8) | (x2 << 16) | (x3 << 24);
 }
 
+// Copies a region of C 16-byte chunks into LDS with direct global -> LDS
+// loads (global_load_lds_dwordx4) by a workgroup of WAVES waves: wave w moves
+// the 64-chunk blocks w, w + WAVES, ...; lane l of block j lands at LDS chunk
+// 64 j + l, and src(x) is the global address of chunk x.  No registers hold
+// the data on its way; the caller waits for vmcnt(0) (wait_vmem) before the
+// barrier that publishes the stage.
+template <int C, int WAVES, typename Src>
+__device__ __forceinline__ void dma_chunks(uint8_t* lds, int wave, int lane, Src src) {
+  static_assert(C % 64 == 0, "whole 64-chunk blocks");
+#pragma unroll
+  for (int j0 = 0; j0 < C / 64; j0 += WAVES) {
+    const int j = j0 + wave;
+    if (C / 64 % WAVES == 0 || j < C / 64)
+      __builtin_amdgcn_global_load_lds(src(j * 64 + lane), lds + j * 1024, 16, 0, 0);
+  }
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left free; gfx9 encoding).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 // Byte offset of the 16-byte piece of row-fragment code storage that holds
 // token `tok`, channels [32*c + 16*h, +16).  See include/sage_mi355x.h.
 __host__ __device__ __forceinline__ int64_t row_frag_offset(int64_t tok, int c, int h, int d) {
