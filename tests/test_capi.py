@@ -144,6 +144,64 @@ def test_producer_entries_reject_bad_arguments(over, status, msg):
     assert msg in lib.sage_last_error().decode()
 
 
+def _bwd_call(lib, **over):
+    a = dict(q=16, k=32, v=48, out=64, lse=80, do=96, b=1, h=2, n=300, d=128, qk=0, smooth=1, sm=0.088,
+             sml=0.1275, mask=None, sz=0, nq=3, nkv=5, doc=None, ws=256, wsb=1 << 30, dq=112, dk=128, dv=144,
+             stream=None)
+    a.update(over)
+    return lib.sage_attn_bwd(a["q"], a["k"], a["v"], a["out"], a["lse"], a["do"], a["b"], a["h"], a["n"], a["d"],
+                             a["qk"], a["smooth"], a["sm"], a["sml"], a["mask"], a["sz"], a["nq"], a["nkv"],
+                             a["doc"], a["ws"], a["wsb"], a["dq"], a["dk"], a["dv"], a["stream"])
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(b=0), 1, "positive"),
+    (dict(n=0), 1, "positive"),
+    (dict(d=96), 1, "head_dim"),
+    (dict(qk=2), 1, "qk_kind"),
+    (dict(h=70000), 1, "grid"),
+    (dict(dq=None), 1, "null"),
+    (dict(lse=None), 1, "null"),
+    (dict(do=40), 2, "aligned"),
+    (dict(sm=0.0), 1, "sm_scale"),
+    (dict(sml=-1.0), 1, "sm_scale"),
+    (dict(mask=256, nkv=4), 1, "block_mask must be 3 x 5"),
+    (dict(mask=256, sz=9), 1, "mask_stride_z"),
+    (dict(ws=None), 3, "workspace"),
+    (dict(wsb=1000), 3, "workspace of"),
+    (dict(ws=264), 2, "workspace must be 16-byte aligned"),
+])
+def test_backward_rejects_bad_arguments(over, status, msg):
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    assert _bwd_call(lib, **over) == status
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_backward_workspace_size():
+    """Codes (1 B), scales (4 B) of Q and K; the K mean; the column-sum
+    partials; five bf16 operand images (dO, Q and K~ transposed, dO and V by
+    row); D (4 B): each region 256-byte aligned."""
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    for b, h, n, d in ((1, 30, 4416, 128), (2, 3, 300, 64), (1, 1, 1, 64)):
+        rows = b * h * ((n + 127) // 128 * 128)
+        up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+        want = (up(rows * d) * 2 + up(rows * 4) * 2 + up(b * h * d * 2) + up(lib.sage_quant_workspace_bytes(b * h, n, d))
+                + up(rows * d * 2) * 5 + up(rows * 4))
+        assert lib.sage_attn_bwd_workspace_bytes(b, h, n, d) == want
+
+
+def test_backward_python_glue_checks():
+    from futudiffu_amd import sage_attention as SA
+    q = torch.zeros(1, 2, 8, 64, dtype=torch.bfloat16)
+    lse = torch.zeros(2, 8)
+    with pytest.raises(ValueError):
+        SA.sage_backward(q, q, q, q, lse, q, qk="int4")
+    with pytest.raises(AssertionError):
+        SA.sage_backward(q.float(), q, q, q, lse, q)
+
+
 def test_fused_quantize_entry_checks_outputs():
     from futudiffu_amd import _lib
     lib = _lib.load()
