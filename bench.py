@@ -94,6 +94,10 @@ CASES = {
     "dit1280x832_bwd_int8": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="bf16", gran="token", bwd=True),
     "packed_tilemask_bwd_int8": dict(B=1, H=30, N=6912, D=128, qk="int8", pv="bf16", gran="token",
                                      segments=[1280, 1216, 4416], mask="tile", bwd=True),
+    "packed_docids_bwd_int8": dict(B=1, H=30, N=6912, D=128, qk="int8", pv="bf16", gran="token",
+                                   segments=[1280, 1216, 4416], mask="doc", bwd=True),
+    "ktuple_b4n4352_keypad_bwd_int8": dict(B=4, H=30, N=4352, D=128, qk="int8", pv="bf16", gran="token",
+                                           mask="keypad", text=256, bwd=True),
 }
 PEAK_MIXED_TFLOPS = 2.0 / (1.0 / PEAK_8BIT_TFLOPS + 1.0 / PEAK_BF16_TFLOPS)  # fp8 QK + bf16 PV
 
@@ -290,13 +294,15 @@ def backward_case(args, name, c):
     sm = 1.0 / math.sqrt(D)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     bmd = None if bm is None else bm.to(dev)
+    docd = None if doc is None else doc.to(dev)
     g = torch.Generator(device="cpu").manual_seed(7)
     dout = torch.randn(B, H, N, D, generator=g).bfloat16()
     dod = dout.to(dev)
-    out, lse = SA.sage_forward(qd, kd, vd, sm, block_mask=bmd, qk=c["qk"], pv=c["pv"], smooth_k=True)
+    out, lse = SA.sage_forward(qd, kd, vd, sm, block_mask=bmd, doc_ids=docd, qk=c["qk"], pv=c["pv"], smooth_k=True)
 
     def step():
-        return SA.sage_backward(qd, kd, vd, out, lse, dod, sm, block_mask=bmd, qk=c["qk"], smooth_k=True)
+        return SA.sage_backward(qd, kd, vd, out, lse, dod, sm, block_mask=bmd, doc_ids=docd, qk=c["qk"],
+                                smooth_k=True)
 
     for _ in range(max(args.warmup // 4, 10)):
         step()
@@ -325,9 +331,11 @@ def backward_case(args, name, c):
         from oracle import sage_oracle as O
         q1, k1, v1, d1 = q[:1, :1], k[:1, :1], v[:1, :1], dout[:1, :1]
         bm1 = None if bm is None else bm
-        o1, l1, _ = O.sage_forward(q1, k1, v1, sm, c["qk"], "bf16", "token", True, bm1)
+        doc1 = None if doc is None else doc[:1]
+        o1, l1, _ = O.sage_forward(q1, k1, v1, sm, c["qk"], "bf16", "token", True, bm1, doc1)
         t0 = time.perf_counter()
-        O.sage_backward(q1, k1, v1, o1, l1, d1, sm, qk=c["qk"], smooth=True, block_mask=bm1, head_chunk=1)
+        O.sage_backward(q1, k1, v1, o1, l1, d1, sm, qk=c["qk"], smooth=True, block_mask=bm1, doc_ids=doc1,
+                        head_chunk=1)
         per_head = time.perf_counter() - t0
         line["cpu_baseline"] = {
             "value": round(flop / (B * H) / per_head / 1e12, 6), "unit": "TFLOP/s",

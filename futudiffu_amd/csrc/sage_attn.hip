@@ -46,19 +46,6 @@ namespace sage {
 constexpr float kLog2Fp8Max = 8.807354922057604f;  // log2(448)
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 
-// Tile class for a block of queries against one key tile:
-// 0 = nothing visible, 1 = everything visible, 2 = per-token mask needed.
-// Summaries are (min doc, max doc, #valid tokens, #padding tokens) over
-// tokens below N; padded queries (doc < 0) see every valid key.
-__device__ __forceinline__ int classify(int4 qsum, int4 ksum) {
-  if (qsum.z + qsum.w == 0) return 0;           // no query row below N
-  if (ksum.z == 0) return 0;                    // no valid key
-  if (qsum.z == 0) return ksum.w == 0 ? 1 : 2;  // only padded queries: they see every valid key
-  if (qsum.w == 0 && (qsum.y < ksum.x || ksum.y < qsum.x)) return 0;
-  if (ksum.w == 0 && ksum.x == ksum.y && qsum.x == qsum.y && qsum.x == ksum.x) return 1;
-  return 2;
-}
-
 // Per-batch token summaries: kv tiles of 64, query blocks of 32 and of 128.
 // One wave per summary (grid-stride over summaries): lane l reads tokens
 // t0 + l and t0 + 64 + l, then wave-wide min / max / sums.
@@ -812,14 +799,23 @@ hipError_t launch_attn_d(int qk, int pv, int gran, int mask, const AttnParams& p
   return hipErrorInvalidValue;
 }
 
+hipError_t launch_doc_summaries(const int32_t* doc, int64_t n, int nb, int4* kv_sum, int4* q_sum, int4* q_sum128,
+                                hipStream_t st) {
+  const int64_t np = padded_len(n);
+  const int nt = (int)((n + 63) / 64);
+  const int64_t total = (int64_t)nb * (nt + np / 32 + np / 128);  // summaries, one wave each
+  const int64_t blocks = (total + 3) / 4 < 8192 ? (total + 3) / 4 : 8192;
+  hipLaunchKernelGGL(doc_summary_kernel, dim3((unsigned)blocks), dim3(256), 0, st, doc, n, np, nb, nt, kv_sum, q_sum,
+                     q_sum128);
+  return hipGetLastError();
+}
+
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb,
                        hipStream_t st) {
   if (mask & 2) {
-    const int64_t total = (int64_t)nb * (p.nt + p.np / 32 + p.np / 128);  // summaries, one wave each
-    const int64_t blocks = (total + 3) / 4 < 8192 ? (total + 3) / 4 : 8192;
-    hipLaunchKernelGGL(doc_summary_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p.doc, p.n,
-                       p.np, nb, p.nt, const_cast<int4*>(p.kv_sum), const_cast<int4*>(p.q_sum),
-                       const_cast<int4*>(p.q_sum128));
+    const hipError_t e = launch_doc_summaries(p.doc, p.n, nb, const_cast<int4*>(p.kv_sum),
+                                              const_cast<int4*>(p.q_sum), const_cast<int4*>(p.q_sum128), st);
+    if (e != hipSuccess) return e;
   }
   if (d == 128) return launch_attn_d<128>(qk, pv, gran, mask, p, st);
   if (d == 64) return launch_attn_d<64>(qk, pv, gran, mask, p, st);

@@ -283,9 +283,17 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) acc[c] = f32x16{0};
 
+  // document-id summaries: the workgroup's 128 queries and this wave's 32
+  int4 qsum128 = make_int4(0, 0, 0, 0), qsum32 = make_int4(0, 0, 0, 0);
+  if constexpr (MASK & 2) {
+    qsum128 = p.q_sum128[(int64_t)bidx * nq + qt];
+    qsum32 = p.q_sum[(int64_t)bidx * (np / 32) + (q0 >> 5)];
+  }
   auto active = [&](int t) __attribute__((always_inline)) -> bool {
-    if constexpr (MASK & 1) return p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] != 0;
-    return true;
+    bool on = true;
+    if constexpr (MASK & 1) on = p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] != 0;
+    if constexpr (MASK & 2) on = on && classify(qsum128, p.kv_sum[(int64_t)bidx * nt + t]) != 0;
+    return on;
   };
   auto next_active = [&](int t) __attribute__((always_inline)) -> int {
     while (t < nt && !active(t)) ++t;
@@ -331,7 +339,9 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
   while (t < nt) {
     const int tn = next_active(t + 1);
     if (tn < nt) load_tile(tn, stage ^ 1);
-    if (wave_live) {
+    bool wave_on = wave_live;
+    if constexpr (MASK & 2) wave_on = wave_on && classify(qsum32, p.kv_sum[(int64_t)bidx * nt + t]) != 0;
+    if (wave_on) {
       const uint8_t* sb = smem + stage * St::bytes;
       // S^T = K . Q^T for keys 32b + (lane-local rows) x this wave's queries
       i32x4 ka[NC];
@@ -503,16 +513,31 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
   }
 
   const uint8_t* mrow = (MASK & 1) ? p.tile_mask + (int64_t)bh * p.mask_stride_z : nullptr;
+  // document-id summaries of the workgroup's two key tiles
+  const int4* qs32 = (MASK & 2) ? p.q_sum + (int64_t)bidx * (np / 32) : nullptr;
+  int4 ksum[2] = {make_int4(0, 0, 0, 0), make_int4(0, 0, 0, 0)};
+  if constexpr (MASK & 2) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      ksum[i] = 2 * kb + i < nkv ? p.kv_sum[(int64_t)bidx * nkv + 2 * kb + i] : make_int4(0x7fffffff, -0x7fffffff, 0, 0);
+  }
   auto wave_active = [&](int s) __attribute__((always_inline)) -> bool {
-    if constexpr (MASK & 1) return my_tile < nkv && mrow[(int64_t)(s >> 1) * p.mask_nkv + my_tile] != 0;
-    return true;
+    bool on = true;
+    if constexpr (MASK & 1) on = my_tile < nkv && mrow[(int64_t)(s >> 1) * p.mask_nkv + my_tile] != 0;
+    if constexpr (MASK & 2) on = on && classify(qs32[2 * s + a], ksum[kg >> 1]) != 0;
+    return on;
   };
   auto active = [&](int s) __attribute__((always_inline)) -> bool {
+    bool on = true;
     if constexpr (MASK & 1) {
       const uint8_t* m = mrow + (int64_t)(s >> 1) * p.mask_nkv;
-      return m[2 * kb] != 0 || (2 * kb + 1 < nkv && m[2 * kb + 1] != 0);
+      on = m[2 * kb] != 0 || (2 * kb + 1 < nkv && m[2 * kb + 1] != 0);
     }
-    return true;
+    if constexpr (MASK & 2) {
+      const int4 q64 = merge_summary(qs32[2 * s], qs32[2 * s + 1]);
+      on = on && (classify(q64, ksum[0]) != 0 || classify(q64, ksum[1]) != 0);
+    }
+    return on;
   };
   auto next_active = [&](int s) __attribute__((always_inline)) -> int {
     while (s < nsteps && !active(s)) ++s;

@@ -104,10 +104,10 @@ int check_producer(const void* qkv, const float* q_norm_w, const float* k_norm_w
 // Backward workspace: byte offsets of the quantization's outputs (codes,
 // scales, K mean, column-sum partials), the T images of dO, Q and K~, and D.
 struct BwdWorkspace {
-  size_t qc, qs, kc, ks, kmean, quant, tdo, tq, tk, rdo, rv, delta, bytes;
+  size_t qc, qs, kc, ks, kmean, quant, tdo, tq, tk, rdo, rv, delta, sums, bytes;
 };
 
-BwdWorkspace bwd_workspace(int64_t bh, int64_t n, int64_t d) {
+BwdWorkspace bwd_workspace(int64_t b, int64_t bh, int64_t n, int64_t d) {
   const size_t np = (size_t)sage::padded_len(n), rows = (size_t)bh * np;
   BwdWorkspace w;
   size_t off = 0;
@@ -128,6 +128,8 @@ BwdWorkspace bwd_workspace(int64_t bh, int64_t n, int64_t d) {
   w.rdo = take(rows * d * 2);
   w.rv = take(rows * d * 2);
   w.delta = take(rows * 4);
+  // document-id summaries (used with doc_ids): key tiles, 32- and 128-row blocks
+  w.sums = take((size_t)b * ((n + 63) / 64 + np / 32 + np / 128) * sizeof(int4));
   w.bytes = off;
   return w;
 }
@@ -278,7 +280,7 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
 }
 
 size_t sage_attn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) {
-  return bwd_workspace(b * h, n, d).bytes;
+  return bwd_workspace(b, b * h, n, d).bytes;
 }
 
 int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, const float* lse, const void* dout,
@@ -308,7 +310,7 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
   if (doc_ids) mask |= 2;
   if ((b * h) * ((n + 127) / 128) > 0x7fffffff)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(b * h * ((n + 127) / 128)));
-  const BwdWorkspace ws = bwd_workspace(b * h, n, d);
+  const BwdWorkspace ws = bwd_workspace(b, b * h, n, d);
   if (!workspace || workspace_bytes < ws.bytes)
     return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", ws.bytes, workspace_bytes);
   if (!aligned16(workspace)) return fail(SAGE_ERR_ALIGN, "workspace must be 16-byte aligned");
@@ -339,6 +341,13 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
   e = sage::launch_bwd_prep(jobs, rjobs, do16, static_cast<const uint16_t*>(out), bh, n, d,
                             reinterpret_cast<float*>(w + ws.delta), stream);
   if (e != hipSuccess) return launch_status(e, "sage_attn_bwd (prep)");
+  const int4* sums = reinterpret_cast<const int4*>(w + ws.sums);
+  const int64_t np = sage::padded_len(n);
+  if (doc_ids) {
+    e = sage::launch_doc_summaries(doc_ids, n, (int)b, const_cast<int4*>(sums), const_cast<int4*>(sums + b * nkv),
+                                   const_cast<int4*>(sums + b * nkv + b * (np / 32)), stream);
+    if (e != hipSuccess) return launch_status(e, "sage_attn_bwd (summaries)");
+  }
   sage::BwdParams p;
   memset(&p, 0, sizeof(p));
   p.qc = w + ws.qc;
@@ -358,11 +367,14 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
   p.mask_stride_z = mask_stride_z;
   p.mask_nkv = mask_nkv;
   p.doc = doc_ids;
+  p.kv_sum = sums;
+  p.q_sum = sums + b * nkv;
+  p.q_sum128 = sums + b * nkv + b * (np / 32);
   p.dq = static_cast<uint16_t*>(dq);
   p.dk = static_cast<uint16_t*>(dk);
   p.dv = static_cast<uint16_t*>(dv);
   p.n = n;
-  p.np = sage::padded_len(n);
+  p.np = np;
   p.h = (int)h;
   p.sm_scale = sm_scale;
   return launch_status(sage::launch_bwd(qk_kind, mask, p, d, bh, stream), "sage_attn_bwd");

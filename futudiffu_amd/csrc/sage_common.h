@@ -56,6 +56,25 @@ __device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d
   return x0 | (x1 << 8) | (x2 << 16) | (x3 << 24);
 }
 
+// Tile class for a block of queries against one key tile:
+// 0 = nothing visible, 1 = everything visible, 2 = per-token mask needed.
+// Summaries are (min doc, max doc, #valid tokens, #padding tokens) over
+// tokens below N (an empty one is (INT_MAX, -INT_MAX, 0, 0)); padded queries
+// (doc < 0) see every valid key.
+__device__ __forceinline__ int classify(int4 qsum, int4 ksum) {
+  if (qsum.z + qsum.w == 0) return 0;           // no query row below N
+  if (ksum.z == 0) return 0;                    // no valid key
+  if (qsum.z == 0) return ksum.w == 0 ? 1 : 2;  // only padded queries: they see every valid key
+  if (qsum.w == 0 && (qsum.y < ksum.x || ksum.y < qsum.x)) return 0;
+  if (ksum.w == 0 && ksum.x == ksum.y && qsum.x == qsum.y && qsum.x == ksum.x) return 1;
+  return 2;
+}
+
+// Summary of the union of two token blocks.
+__device__ __forceinline__ int4 merge_summary(int4 a, int4 b) {
+  return make_int4(min(a.x, b.x), max(a.y, b.y), a.z + b.z, a.w + b.w);
+}
+
 // Copies a region of C 16-byte chunks into LDS with direct global -> LDS
 // loads (global_load_lds_dwordx4) by a workgroup of WAVES waves: wave w moves
 // the 64-chunk blocks w, w + WAVES, ...; lane l of block j lands at LDS chunk

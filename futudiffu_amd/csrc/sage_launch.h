@@ -99,6 +99,11 @@ hipError_t launch_qkv_postprocess(const ProdArgs& prod, int64_t bh, int64_t n, i
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
 
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb, hipStream_t st);
+// Per-batch document-id summaries (min doc, max doc, #valid, #padding) of every
+// 64-key tile ([nb][ceil(n/64)]), 32-row block ([nb][Np/32]) and 128-row block
+// ([nb][Np/128]).
+hipError_t launch_doc_summaries(const int32_t* doc, int64_t n, int nb, int4* kv_sum, int4* q_sum, int4* q_sum128,
+                                hipStream_t st);
 // Workspace of one attention call: the doc-id summaries, then the partial
 // slots of the tail split.
 struct AttnWorkspace {
@@ -134,7 +139,10 @@ struct BwdParams {
   const uint8_t* tile_mask;
   int64_t mask_stride_z;
   int64_t mask_nkv;
-  const int32_t* doc;  // [B, N] document ids (mask bit 2)
+  const int32_t* doc;     // [B, N] document ids (mask bit 2)
+  const int4* kv_sum;     // their summaries: [B][ceil(N/64)] key tiles,
+  const int4* q_sum;      // [B][Np/32] and [B][Np/128] query blocks
+  const int4* q_sum128;
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;

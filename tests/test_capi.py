@@ -181,7 +181,8 @@ def test_backward_rejects_bad_arguments(over, status, msg):
 def test_backward_workspace_size():
     """Codes (1 B), scales (4 B) of Q and K; the K mean; the column-sum
     partials; five bf16 operand images (dO, Q and K~ transposed, dO and V by
-    row); D (4 B): each region 256-byte aligned."""
+    row); D (4 B); the document-id summaries (16 B per 64-key tile and per
+    32- and 128-row block of each batch): each region 256-byte aligned."""
     from futudiffu_amd import _lib
     lib = _lib.load()
     for b, h, n, d in ((1, 30, 4416, 128), (2, 3, 300, 64), (1, 1, 1, 64)):
@@ -189,6 +190,8 @@ def test_backward_workspace_size():
         up = lambda x: (x + 255) // 256 * 256  # noqa: E731
         want = (up(rows * d) * 2 + up(rows * 4) * 2 + up(b * h * d * 2) + up(lib.sage_quant_workspace_bytes(b * h, n, d))
                 + up(rows * d * 2) * 5 + up(rows * 4))
+        np_ = (n + 127) // 128 * 128
+        want += up(b * ((n + 63) // 64 + np_ // 32 + np_ // 128) * 16)
         assert lib.sage_attn_bwd_workspace_bytes(b, h, n, d) == want
 
 
