@@ -7,11 +7,11 @@
 // the fp8-QK kernels (:356-590); launchers sage_attention.py:344-458, :534-648.
 //
 // Operands.  P is recomputed from the forward's per-token codes exactly as the
-// forward scores them: s = (acc * qd) * kd (qd carrying sm_scale*log2(e)),
+// forward scores them, s = acc * qd * kd (qd carrying sm_scale*log2(e)),
 // p = 2^(s - lse) with the forward's base-2 LSE.  The quantization kernel
 // supplies the Q and smoothed-K codes and scales and, given dO in place of V,
-// the T image of dO; timage_kernel writes the T images of Q and K~ and
-// delta_kernel D = rowsum(dO * O).
+// the T image of dO; timage_kernel writes the T images of Q and K~,
+// rimage_kernel the R images of dO and V, delta_kernel D = rowsum(dO * O).
 //
 // T image of bf16 rows X [N, D]: per 64-token block, chunks (j, b, tt) of 64
 // lanes x 8 bf16, element 4jj + i of lane 32hh + r holding
@@ -20,25 +20,33 @@
 // comes straight from a 32x32 accumulator (lane (h, r) holding rows
 // 8J + 4h + i, element 4J + i): lane half h supplies the same 8 tokens to both
 // operands.  The forward's bf16 V operand is the T image of V.
+// R image: per 32-token block and 16-channel group, lane (h, r) holds the 16
+// bytes X[r][8h, +8) of the group: the row operand of the same instruction for
+// a contraction over channels.
 //
-// dQ kernel: a workgroup is the forward's 128-query tile, 4 waves x 32
-// queries, streaming 64-key tiles through a two-stage LDS ring (registers
-// carry tile i+1 from global memory while tile i is consumed; one barrier per
-// tile).  Per wave and tile, in the S^T layout (lane (h, r) = query r, keys
-// 8J + 4h + i):
+// Workgroups have 8 waves, two per SIMD; stages pass through a two-stage LDS
+// ring filled by direct global -> LDS loads issued one stage ahead (one
+// barrier per stage).  Work items are dealt to XCDs in contiguous ranges.
+//
+// dQ kernel: a workgroup is the forward's 128-query tile; wave w takes queries
+// 32 (w % 4) and key half w / 4 of every 64-key tile.  Per wave and tile, in
+// the S^T layout (lane (h, r) = query r, keys 8J + 4h + i):
 //   S^T = K . Q^T (int8 / fp8 MFMA, the forward's operands),
-//   dP^T = V . dO^T (bf16 MFMA; V rows from LDS, the wave's dO rows in registers),
-//   dS^T = P^T (dP^T - D), dQ += dS . K~ (A = dS from the registers, B = T image of K~),
-// and dQ * sm_scale is rounded to bf16 at the end (sage_kernels.py:1720).
-// dK/dV kernel: a workgroup owns 128 keys, 32 per wave, and streams 64-query
-// steps.  Per wave and step, in the S layout (lane (h, r) = key r, queries
-// 8J + 4h + i):
+//   dP^T = V . dO^T (bf16 MFMA; V from the stage, the wave's dO rows in registers),
+//   dS^T = P^T (dP^T - D), dQ += dS . K~ (A = dS from the registers, B = T image of K~);
+// the two key halves' dQ are added, then dQ * sm_scale is rounded to bf16
+// (sage_kernels.py:1720).
+// dK/dV kernel: a workgroup owns 128 keys; wave w takes keys 32 (w % 4) and
+// query half w / 4 of every 64-query step.  Per wave and step, in the S
+// layout (lane (h, r) = key r, queries 8J + 4h + i):
 //   S = Q . K^T and dP = dO . V^T (the wave's K codes in registers, the
 //   workgroup's V rows in LDS for the whole launch),
 //   dS = P (dP - D), dV^T += dO^T . bf16(P), dK^T += Q^T . bf16(dS * sm_scale)
-// (A = the T images of dO and Q, B = P and dS from the registers).
+// (A = the T images of dO and Q, B = P and dS from the registers); the two
+// query halves' dK and dV are added at the end.
 // Both kernels skip (query tile, key tile) pairs the reference tile mask turns
-// off; with document ids, hidden pairs get p = 0.
+// off; with document ids they skip pairs whose summaries show no visible pair
+// and give hidden pairs p = 0.
 #include <type_traits>
 
 #include "sage_common.h"
@@ -54,8 +62,7 @@ __device__ __forceinline__ uint32_t word_at(const uint4& w, int i) {
 
 __device__ __forceinline__ uint4 zero_if(bool z, uint4 w) { return z ? make_uint4(0, 0, 0, 0) : w; }
 
-// 16-byte staging unit as a native vector: copies are plain loads and stores,
-// so arrays of them stay in registers.
+// 16-byte unit as a native vector: its copies are plain loads and stores.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int QK>
@@ -469,8 +476,8 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
   using St = DkvStage<D>;
   using SAcc = typename BAcc<QK>::type;
   constexpr int NC = D / 32, CPR = D / 8;
-  // two step stages, then the workgroup's 128 V rows (swizzled), read as the
-  // B operand of dP by the waves that own them
+  // two step stages, then the R image of the workgroup's 128 V rows, read as
+  // the B operand of dP by the waves that own them
   constexpr int kVOff = 2 * St::bytes;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kVOff + kRowsPerWG * 2 * D];
   static_assert(4 * NC * 16 * 64 * 4 <= 2 * St::bytes, "partial dK/dV exchange must fit in the ring");
