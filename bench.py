@@ -98,6 +98,10 @@ CASES = {
                                    segments=[1280, 1216, 4416], mask="doc", bwd=True),
     "ktuple_b4n4352_keypad_bwd_int8": dict(B=4, H=30, N=4352, D=128, qk="int8", pv="bf16", gran="token",
                                            mask="keypad", text=256, bwd=True),
+    # the producer's backward (RMSNorm + rotary gradients into the QKV
+    # projection layout) at the 1280x832 shape
+    "dit1280x832_producer_bwd": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="bf16", gran="token",
+                                     producer_bwd=True),
 }
 PEAK_MIXED_TFLOPS = 2.0 / (1.0 / PEAK_8BIT_TFLOPS + 1.0 / PEAK_BF16_TFLOPS)  # fp8 QK + bf16 PV
 
@@ -346,6 +350,59 @@ def backward_case(args, name, c):
     print(json.dumps(line), flush=True)
 
 
+def producer_backward_case(args, name, c):
+    """Time the producer's backward (``qkv_postprocess_backward``).
+    Algorithmic bytes: the q and k rows of the projection output and the
+    three incoming gradients read (5 * B*N*H*D bf16), the three rotation
+    entries per channel pair and token read once (12 * B*N*D/2), dqkv written
+    (3 * B*N*H*D bf16)."""
+    from futudiffu_amd import sage_attention as SA
+    dev = torch.device("cuda:0")
+    B, H, N, D = c["B"], c["H"], c["N"], c["D"]
+    g = torch.Generator(device="cpu").manual_seed(3)
+    qkv = torch.randn(B, N, 3 * H * D, generator=g).bfloat16()
+    nw = 1.0 + 0.1 * torch.randn(2, D, generator=g)
+    ang = torch.rand(B, N, 1, D // 2, generator=g) * 6.283
+    cs, sn = torch.cos(ang), torch.sin(ang)
+    freqs = torch.stack([torch.stack([cs, -sn], -1), torch.stack([sn, cs], -1)], -2)
+    grads = [torch.randn(B, H, N, D, generator=g).bfloat16() for _ in range(3)]
+    dv = [t.to(dev) for t in (qkv, nw[0], nw[1], freqs, *grads)]
+
+    def step():
+        return SA.qkv_postprocess_backward(*dv, H, D, 1e-5)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = 5 * B * N * H * D * 2 + 12 * B * N * (D // 2) + 3 * B * N * H * D * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    line = {
+        "case": name,
+        "config": {k2: v2 for k2, v2 in c.items()},
+        "producer_bwd_ms": round(ms, 5),
+        "bytes": nbytes,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4)},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import sage_oracle as O
+        t0 = time.perf_counter()
+        O.qkv_postprocess_backward(qkv, nw[0], nw[1], freqs, *grads, H, D, 1e-5)
+        sec = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"oracle producer backward (torch CPU, fp64) on the whole case: "
+                                      f"{sec * 1e3:.1f} ms", "cpu_model": _cpu_model()}
+    print(json.dumps(line), flush=True)
+
+
 def all_configs(args):
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from futudiffu_amd import sage_attention as SA
@@ -357,6 +414,9 @@ def all_configs(args):
         print(f"# case {name}", file=sys.stderr, flush=True)
         if c.get("bwd"):
             backward_case(args, name, c)
+            continue
+        if c.get("producer_bwd"):
+            producer_backward_case(args, name, c)
             continue
         q, k, v, bm, doc, flop, extra = _case_inputs(c, dev)
         qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)

@@ -32,6 +32,8 @@ SIGNATURES = {
     "sage_qk_int32": (_c.c_int, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "sage_build_tile_mask": (_c.c_int, [_P, _I64, _I64, _c.c_int32, _P, _P]),
     "sage_qkv_postprocess": (_c.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_float, _P, _P, _P, _P]),
+    "sage_qkv_postprocess_bwd": (_c.c_int, [
+        _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_float, _P, _P]),
     "sage_quantize_from_qkv": (_c.c_int, [
         _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_float, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_float,
         _P, _P, _P, _P, _P, _P, _P, _P, _c.c_size_t, _P]),

@@ -28,8 +28,9 @@ the out-projection that follows it (transformer.py:471).
 (fused_qkv_postprocess, transformer.py:459-463): it reads the QKV projection
 output and quantizes inside the producer, so bf16 q, k, v never reach HBM.
 The extension ops differentiate through ``futudiffu_ii::sage_bwd_ext``, with
-the forward's variant; ``sage_attn_qkv_masked`` has no backward (the
-producer's RMSNorm / rotary backward is not built) and raises if asked.
+the forward's variant; ``sage_attn_qkv_masked`` differentiates with respect to
+``qkv`` through the attention backward and the producer's analytical backward
+(fused_kernels.py:711-783).
 """
 
 from __future__ import annotations
@@ -210,16 +211,6 @@ def _ext_backward(ctx, grad_out, grad_lse):
 sage_attn_ext_op.register_autograd(_ext_backward, setup_context=_ext_setup_context)
 
 
-def _no_backward(ctx, grad_out, grad_lse):
-    raise NotImplementedError("sage_attn_qkv_masked has no backward: the q/k/v producer's RMSNorm and "
-                              "rotary backward is not built; differentiate fused_qkv_postprocess followed "
-                              "by sage_attn_masked instead")
-
-
-def _no_setup_context(ctx, inputs, output):
-    pass
-
-
 # JointAttention.forward (transformer.py:467-471) calls sage_attn_masked and
 # then out.transpose(1, 2).reshape(b, -1, H*D) for its out-projection.  This op
 # returns that [B, N, H*D] tensor directly (the kernel stores rows in that
@@ -266,4 +257,25 @@ def _fake_qkv_masked(qkv, q_norm_weight, k_norm_weight, freqs_cis, block_mask, n
     return qkv.new_empty(B, N, n_heads * head_dim), qkv.new_empty(B * n_heads, N, dtype=torch.float32)
 
 
-sage_attn_qkv_masked_op.register_autograd(_no_backward, setup_context=_no_setup_context)
+def _qkv_masked_setup(ctx, inputs, output):
+    qkv, q_norm_weight, k_norm_weight, freqs_cis, block_mask, n_heads, head_dim, norm_eps, sm_scale = inputs
+    out, lse = output
+    ctx.save_for_backward(qkv, q_norm_weight, k_norm_weight, freqs_cis, block_mask, out, lse)
+    ctx.args = (n_heads, head_dim, norm_eps, sm_scale)
+
+
+def _qkv_masked_backward(ctx, grad_out, grad_lse):
+    """The producer's outputs are recomputed (bit-identical to the ones the
+    fused forward quantized), then the attention backward (int8 P
+    recomputation, as the forward) and the producer's backward."""
+    qkv, qw, kw, freqs, block_mask, out, lse = ctx.saved_tensors
+    n_heads, head_dim, norm_eps, sm_scale = ctx.args
+    q, k, v = _sa.qkv_postprocess(qkv, qw, kw, freqs, n_heads, head_dim, norm_eps)
+    shape = q.shape
+    dq, dk, dv = sage_bwd_ext_op(q, k, v, _to_bhnd(out, shape), lse, _to_bhnd(grad_out, shape), block_mask, None,
+                                 sm_scale, "int8", True)
+    dqkv = _sa.qkv_postprocess_backward(qkv, qw, kw, freqs, dq, dk, dv, n_heads, head_dim, norm_eps)
+    return dqkv, None, None, None, None, None, None, None, None
+
+
+sage_attn_qkv_masked_op.register_autograd(_qkv_masked_backward, setup_context=_qkv_masked_setup)

@@ -175,6 +175,23 @@ int sage_qkv_postprocess(const void* qkv, const float* q_norm_w, const float* k_
                        "sage_qkv_postprocess");
 }
 
+int sage_qkv_postprocess_bwd(const void* qkv, const float* q_norm_w, const float* k_norm_w, const float* freqs,
+                             const void* grad_q, const void* grad_k, const void* grad_v, int64_t b, int64_t h,
+                             int64_t n, int64_t d, float norm_eps, void* dqkv, hipStream_t stream) {
+  sage::ProdArgs prod;
+  int st = check_producer(qkv, q_norm_w, k_norm_w, freqs, b, h, n, d, norm_eps, prod);
+  if (st) return st;
+  if (!grad_q || !grad_k || !grad_v || !dqkv) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  const void* ptrs[] = {grad_q, grad_k, grad_v, dqkv};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
+  return launch_status(sage::launch_qkv_postprocess_bwd(prod, b * h, n, d, static_cast<const uint16_t*>(grad_q),
+                                                        static_cast<const uint16_t*>(grad_k),
+                                                        static_cast<const uint16_t*>(grad_v),
+                                                        static_cast<uint16_t*>(dqkv), stream),
+                       "sage_qkv_postprocess_bwd");
+}
+
 int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* k_norm_w, const float* freqs,
                            int64_t b, int64_t h, int64_t n, int64_t d, float norm_eps, int qk_kind, int pv_kind,
                            int granularity, int smooth_k, float sm_scale_log2e, void* q_codes, float* q_scale,

@@ -96,6 +96,10 @@ hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t
                            uint16_t* kmean, const ProdArgs& prod, hipStream_t st);
 hipError_t launch_qkv_postprocess(const ProdArgs& prod, int64_t bh, int64_t n, int64_t d, uint16_t* q_out,
                                   uint16_t* k_out, uint16_t* v_out, hipStream_t st);
+// Gradient of the producer with respect to its input (fused_kernels.py:711-783):
+// gq, gk, gv bf16 [BH, N, D] -> dqkv bf16 [B, N, 3*H*D].
+hipError_t launch_qkv_postprocess_bwd(const ProdArgs& prod, int64_t bh, int64_t n, int64_t d, const uint16_t* gq,
+                                      const uint16_t* gk, const uint16_t* gv, uint16_t* dqkv, hipStream_t st);
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
 
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb, hipStream_t st);

@@ -286,6 +286,85 @@ __global__ void __launch_bounds__(256) qkv_postprocess_kernel(ProdArgs prod, int
   }
 }
 
+// Gradient of the producer with respect to the projection output
+// (fused_kernels.py:711-783): per head and token, g' = the rotation's
+// transpose applied to the incoming gradient (:736-758), then the RMSNorm
+// backward dx = rrms * (g'w - x * rrms^2 * sum(g'w * x) / D) (:760-776) for q
+// and k; v's gradient passes through; all written in the [B, N, 3*H*D]
+// layout (:778-783).  fp32 arithmetic with fp64 row sums (8 channels per lane,
+// then the token's lanes); the norm weights and rotations get no gradient, as
+// in the reference.  One workgroup per (64-token block, head), head fastest;
+// lane (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps.
+template <int D>
+__global__ void __launch_bounds__(256) qkv_postprocess_bwd_kernel(ProdArgs prod, int64_t n,
+                                                                  const uint16_t* __restrict__ gq,
+                                                                  const uint16_t* __restrict__ gk,
+                                                                  const uint16_t* __restrict__ gv,
+                                                                  uint16_t* __restrict__ dqkv) {
+  constexpr int LPR = D / 8;
+  constexpr int RPP = 256 / LPR;
+  constexpr int PASSES = 64 / RPP;
+  int64_t unit;
+  int bh;
+  block_coords<true>(prod, unit, bh);
+  const int tid = threadIdx.x;
+  const int c8 = tid % LPR, rr = tid / LPR;
+  const int64_t tok0 = unit * 64;
+  const HeadRows<D, true> src(nullptr, nullptr, nullptr, prod, bh, n);
+  const int64_t head_off = (int64_t)(bh % prod.h) * D;  // the head's column offset in each third
+  const int64_t third = (int64_t)prod.h * D;
+  float qn[8], kn[8];
+  load_w8(prod.qw, c8, qn);
+  load_w8(prod.kw, c8, kn);
+  auto one = [&](uint4 xw, uint4 gw, const float (&w)[8], const f32x4 (&fr)[4]) __attribute__((always_inline)) {
+    float x[8], g[8], gp[8];
+    unpack8(xw, x);
+    unpack8(gw, g);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {  // transpose of [[cos, -sin], [sin, cos]]
+      const float c = fr[p][0], sn = fr[p][2];
+      gp[2 * p] = (c * g[2 * p] + sn * g[2 * p + 1]) * w[2 * p];
+      gp[2 * p + 1] = (c * g[2 * p + 1] - sn * g[2 * p]) * w[2 * p + 1];
+    }
+    double ss = 0.0, gx = 0.0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ss = __builtin_fma((double)x[e], (double)x[e], ss);
+      gx = __builtin_fma((double)gp[e], (double)x[e], gx);
+    }
+    ss = token_sum<LPR>(ss);
+    gx = token_sum<LPR>(gx);
+    const float rrms = 1.0f / sqrtf((float)(ss / (double)D) + prod.eps);
+    const float cr = (float)(gx / (double)D) * rrms * rrms;
+    uint32_t o[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      o[p] = pack_bf16x2(rrms * (gp[2 * p] - x[2 * p] * cr), rrms * (gp[2 * p + 1] - x[2 * p + 1] * cr));
+    return make_uint4(o[0], o[1], o[2], o[3]);
+  };
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int64_t t = tok0 + rr + ps * RPP;
+    const int64_t tok = min(t, n - 1);  // clamped: the lanes of a token reduce together
+    const int64_t gofs = ((int64_t)bh * n + tok) * D + c8 * 8;
+    const uint4 xq = *reinterpret_cast<const uint4*>(src.q + tok * src.stride + c8 * 8);
+    const uint4 xk = *reinterpret_cast<const uint4*>(src.k + tok * src.stride + c8 * 8);
+    const uint4 g_q = *reinterpret_cast<const uint4*>(gq + gofs);
+    const uint4 g_k = *reinterpret_cast<const uint4*>(gk + gofs);
+    const uint4 g_v = *reinterpret_cast<const uint4*>(gv + gofs);
+    f32x4 fr[4];
+    load_freqs<D>(prod.freqs, src.row0 + tok, c8, fr);
+    const uint4 dq = one(xq, g_q, qn, fr);
+    const uint4 dk = one(xk, g_k, kn, fr);
+    if (t < n) {
+      uint16_t* row = dqkv + (src.row0 + t) * 3 * third + head_off + c8 * 8;
+      *reinterpret_cast<uint4*>(row) = dq;
+      *reinterpret_cast<uint4*>(row + third) = dk;
+      *reinterpret_cast<uint4*>(row + 2 * third) = g_v;
+    }
+  }
+}
+
 // Tokens per K column-sum chunk.
 constexpr int kSumTokens = 256;
 
@@ -660,6 +739,18 @@ hipError_t launch_qkv_postprocess(const ProdArgs& prod, int64_t bh, int64_t n, i
     hipLaunchKernelGGL(qkv_postprocess_kernel<128>, grid, dim3(256), 0, st, prod, n, q_out, k_out, v_out);
   else if (d == 64)
     hipLaunchKernelGGL(qkv_postprocess_kernel<64>, grid, dim3(256), 0, st, prod, n, q_out, k_out, v_out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_qkv_postprocess_bwd(const ProdArgs& prod, int64_t bh, int64_t n, int64_t d, const uint16_t* gq,
+                                      const uint16_t* gk, const uint16_t* gv, uint16_t* dqkv, hipStream_t st) {
+  const dim3 grid((unsigned)((n + 63) / 64 * bh));  // head fastest (block_coords)
+  if (d == 128)
+    hipLaunchKernelGGL(qkv_postprocess_bwd_kernel<128>, grid, dim3(256), 0, st, prod, n, gq, gk, gv, dqkv);
+  else if (d == 64)
+    hipLaunchKernelGGL(qkv_postprocess_bwd_kernel<64>, grid, dim3(256), 0, st, prod, n, gq, gk, gv, dqkv);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

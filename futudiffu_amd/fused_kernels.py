@@ -5,8 +5,8 @@ Registers the op name, schema and fake implementation of
 producer kernel (``sage_qkv_postprocess``): QKV split + per-head RMSNorm +
 Flux RoPE + transpose, bf16 ``q, k, v`` ``[B, H, N, D]``.  Import this module
 instead of the reference's ``futudiffu.fused_kernels`` (both register the same
-name).  The op is forward-only: its autograd formula raises, where the
-reference registers an analytical backward for LoRA training (:645-).
+name).  Its autograd formula is the reference's analytical backward
+(:711-783) on the GPU: the gradient with respect to ``qkv`` only.
 """
 
 from __future__ import annotations
@@ -14,8 +14,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from .attention_srcii import _no_backward, _setup_context
-from .sage_attention import qkv_postprocess
+from .sage_attention import qkv_postprocess, qkv_postprocess_backward
 
 
 @torch.library.custom_op("futudiffu::fused_qkv_postprocess", mutates_args=())
@@ -31,8 +30,17 @@ def _fake(qkv, q_norm_weight, k_norm_weight, freqs_cis, n_heads, head_dim, norm_
     return tuple(qkv.new_empty(B, n_heads, seq_len, head_dim) for _ in range(3))
 
 
-def _no_backward3(ctx, gq, gk, gv):
-    return _no_backward(ctx, gq, gk)
+def _setup(ctx, inputs, output):
+    qkv, q_norm_weight, k_norm_weight, freqs_cis, n_heads, head_dim, norm_eps = inputs
+    ctx.save_for_backward(qkv, q_norm_weight, k_norm_weight, freqs_cis)
+    ctx.args = (n_heads, head_dim, norm_eps)
 
 
-fused_qkv_postprocess.register_autograd(_no_backward3, setup_context=_setup_context)
+def _backward(ctx, grad_q, grad_k, grad_v):
+    qkv, qw, kw, freqs = ctx.saved_tensors
+    n_heads, head_dim, norm_eps = ctx.args
+    dqkv = qkv_postprocess_backward(qkv, qw, kw, freqs, grad_q, grad_k, grad_v, n_heads, head_dim, norm_eps)
+    return dqkv, None, None, None, None, None, None
+
+
+fused_qkv_postprocess.register_autograd(_backward, setup_context=_setup)

@@ -196,6 +196,26 @@ def qkv_postprocess(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, f
     return out[0], out[1], out[2]
 
 
+def qkv_postprocess_backward(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, freqs_cis: Tensor,
+                             grad_q: Tensor, grad_k: Tensor, grad_v: Tensor, n_heads: int, head_dim: int,
+                             norm_eps: float = 1e-5) -> Tensor:
+    """Gradient of ``qkv_postprocess`` with respect to ``qkv`` (bf16
+    ``[B, N, 3*H*D]``), given the gradients of its outputs ``[B, H, N, D]``:
+    the reference's analytical backward (fused_kernels.py:711-783) on the GPU."""
+    shape = (qkv.shape[0], n_heads, qkv.shape[1], head_dim)
+    for name, g in (("grad_q", grad_q), ("grad_k", grad_k), ("grad_v", grad_v)):
+        if tuple(g.shape) != shape:
+            raise ValueError(f"{name} must be {list(shape)}, got {tuple(g.shape)}")
+    B, N, qw, kw, fr = _check_producer(qkv, q_norm_weight, k_norm_weight, freqs_cis, n_heads, head_dim)
+    gs = [g.to(device=qkv.device, dtype=torch.bfloat16).contiguous() for g in (grad_q, grad_k, grad_v)]
+    dqkv = torch.empty_like(qkv)
+    lib = _lib.load()
+    _lib.check(lib.sage_qkv_postprocess_bwd(
+        qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), fr.data_ptr(), gs[0].data_ptr(), gs[1].data_ptr(),
+        gs[2].data_ptr(), B, n_heads, N, head_dim, float(norm_eps), dqkv.data_ptr(), _stream_handle(qkv.device)))
+    return dqkv
+
+
 def quantize_from_qkv(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, freqs_cis: Tensor,
                       n_heads: int, head_dim: int, norm_eps: float = 1e-5, sm_scale: float | None = None, *,
                       qk: str = "int8", pv: str = "bf16", granularity: str = "token",

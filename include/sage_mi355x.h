@@ -131,6 +131,24 @@ int sage_qkv_postprocess(const void* qkv, const float* q_norm_w, const float* k_
                          float norm_eps, void* q_out, void* k_out, void* v_out,
                          hipStream_t stream);
 
+/* Gradient of the producer with respect to the projection output.
+ * Replaces the autograd formula of fused_qkv_postprocess
+ * (src/futudiffu/fused_kernels.py:711-783): per token and head, the incoming
+ * q / k gradient through the rotation's transpose, then the RMSNorm backward
+ * rrms * (g*w - x * rrms^2 * sum(g*w * x) / D); v's gradient passes through.
+ * The norm weights and rotations get no gradient, as in the reference.
+ *   qkv, q_norm_w, k_norm_w, freqs, b, h, n, d, norm_eps  as in
+ *                sage_qkv_postprocess (the forward's inputs).
+ *   grad_q,
+ *   grad_k,
+ *   grad_v     bf16 [B, H, N, D] gradients of the producer's outputs.
+ *   dqkv       bf16 [B, N, 3*H*D].
+ * fp32 arithmetic with fp64 row sums.  All pointers 16-byte aligned. */
+int sage_qkv_postprocess_bwd(const void* qkv, const float* q_norm_w, const float* k_norm_w,
+                             const float* freqs, const void* grad_q, const void* grad_k,
+                             const void* grad_v, int64_t b, int64_t h, int64_t n, int64_t d,
+                             float norm_eps, void* dqkv, hipStream_t stream);
+
 /* sage_quantize_qkv applied to the outputs of sage_qkv_postprocess, without
  * writing them: the producer runs inside the quantization kernels, which read
  * the projection output directly (half the HBM traffic of producer +

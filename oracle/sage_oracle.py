@@ -140,6 +140,49 @@ def qkv_postprocess(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.T
     return tuple(t.movedim(1, 2).contiguous() for t in (q, k, v))
 
 
+def qkv_postprocess_backward(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+                             freqs: torch.Tensor, grad_q: torch.Tensor, grad_k: torch.Tensor,
+                             grad_v: torch.Tensor, n_heads: int, head_dim: int,
+                             eps: float = 1e-5) -> torch.Tensor:
+    """Gradient of the producer with respect to ``qkv``, bf16 ``[B, N, 3*H*D]``
+    (fused_kernels.py:711-783; the norm weights and rotations get none, :783).
+
+    Per head and token, with x the raw q (k) row, w its norm weights,
+    rrms = 1/sqrt(mean(x^2) + eps) and g = the incoming gradient (:732-734):
+      * the rotation's transpose, per pair (e, o) with (cos, sin) the matrix
+        entries [0][0] and [1][0]: (cos*g_e + sin*g_o, -sin*g_e + cos*g_o)
+        (:736-758);
+      * the RMSNorm backward: gw = g' * w, c = sum(gw * x) / D,
+        dx = rrms * (gw - x * rrms^2 * c) (:760-776), rounded to bf16;
+      * v's gradient passes through; the three blocks are concatenated in the
+        projection's layout (:778-783).
+    Evaluated in fp64 from the bf16 inputs (the reference uses fp32 with
+    unspecified reduction order: tolerance-level).
+    """
+    b, n, _ = qkv.shape
+    h, d = n_heads, head_dim
+    if freqs.ndim == 6:
+        freqs = freqs.squeeze(2)
+    cos = freqs[..., 0, 0].double()[:, :, None, :]  # [B, N, 1, D/2]
+    sin = freqs[..., 1, 0].double()[:, :, None, :]
+    x = qkv.view(b, n, 3, h, d)
+
+    def one(grad, xr, w):
+        g = grad.movedim(1, 2).double().reshape(b, n, h, d // 2, 2)
+        ge, go = g[..., 0], g[..., 1]
+        gp = torch.stack([cos * ge + sin * go, -sin * ge + cos * go], -1).reshape(b, n, h, d)
+        xf = xr.double()
+        rrms = 1.0 / torch.sqrt((xf * xf).mean(-1, keepdim=True) + eps)
+        gw = gp * w.double()
+        c = (gw * xf).sum(-1, keepdim=True) / d
+        return (rrms * (gw - xf * rrms * rrms * c)).to(torch.bfloat16)
+
+    dq = one(grad_q, x[:, :, 0], q_norm_w)
+    dk = one(grad_k, x[:, :, 1], k_norm_w)
+    dv = grad_v.movedim(1, 2)
+    return torch.cat([dq.reshape(b, n, h * d), dk.reshape(b, n, h * d), dv.reshape(b, n, h * d)], -1).contiguous()
+
+
 # ---------------------------------------------------------------------------
 # K smoothing (sage_attention.py:63-71, called at :490-491)
 # ---------------------------------------------------------------------------

@@ -142,6 +142,31 @@ def test_producer_entries_reject_bad_arguments(over, status, msg):
     assert lib.sage_quantize_from_qkv(*_prod_args(**over), 0, 1, 0, 1, 0.18, 128, 144, 160, 176, 192, 208, 224,
                                       240, 1 << 20, None) == status
     assert msg in lib.sage_last_error().decode()
+    a = _prod_args(**over)
+    assert lib.sage_qkv_postprocess_bwd(*a[:4], 80, 96, 112, *a[4:], 128, None) == status
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_producer_backward_checks_gradient_pointers():
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    a = _prod_args()
+    assert lib.sage_qkv_postprocess_bwd(*a[:4], 80, None, 112, *a[4:], 128, None) == 1
+    assert "null" in lib.sage_last_error().decode()
+    assert lib.sage_qkv_postprocess_bwd(*a[:4], 80, 96, 112, *a[4:], None, None) == 1
+    assert lib.sage_qkv_postprocess_bwd(*a[:4], 80, 96, 120, *a[4:], 128, None) == 2
+    assert "aligned" in lib.sage_last_error().decode()
+    assert lib.sage_qkv_postprocess_bwd(*a[:4], 80, 96, 112, *a[4:], 136, None) == 2
+
+
+def test_producer_backward_python_glue_checks():
+    from futudiffu_amd import sage_attention as SA
+    qkv = torch.zeros(1, 8, 3 * 2 * 64, dtype=torch.bfloat16)
+    w = torch.ones(64)
+    fr = torch.zeros(1, 8, 1, 32, 2, 2)
+    g = torch.zeros(1, 2, 8, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="grad_k must be"):
+        SA.qkv_postprocess_backward(qkv, w, w, fr, g, g[:, :1], g, 2, 64)
 
 
 def _bwd_call(lib, **over):

@@ -129,3 +129,41 @@ def test_sum_of_squares_order_is_runs_of_eight_then_pairwise():
         seq = seq + v
     assert runs[0] == 2.0 ** 60 + 512 and seq == 2.0 ** 60
     assert O.sum_squares(x).item() == runs[0]
+
+
+def _producer_fp64(qkv, qw, kw, freqs, h, d, eps=1e-5):
+    """Differentiable fp64 producer: RMSNorm with weights, then the rotation."""
+    b, n, _ = qkv.shape
+    x = qkv.view(b, n, 3, h, d)
+    f = freqs.squeeze(2).double()[:, :, None]  # [B, N, 1, D/2, 2, 2]
+
+    def one(xr, w):
+        rr = 1.0 / torch.sqrt((xr * xr).mean(-1, keepdim=True) + eps)
+        nn = (xr * rr * w).reshape(b, n, h, d // 2, 2)
+        e = f[..., 0, 0] * nn[..., 0] + f[..., 0, 1] * nn[..., 1]
+        o = f[..., 1, 0] * nn[..., 0] + f[..., 1, 1] * nn[..., 1]
+        return torch.stack([e, o], -1).reshape(b, n, h, d).movedim(1, 2)
+
+    return one(x[:, :, 0], qw.double()), one(x[:, :, 1], kw.double()), x[:, :, 2].movedim(1, 2)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_producer_backward_matches_fp64_autograd(d):
+    """The restated backward (fused_kernels.py:711-783) against autograd of the
+    fp64 producer on the same bf16 input: differences are the bf16 rounding
+    of the result only.  A dropped mean term, a wrong rotation sign or the
+    wrong norm weight moves the result far outside the bound."""
+    b, n, h = 2, 19, 3
+    qkv, qw, kw, freqs = _inputs(b, n, h, d, seed=8, scale=1.5)
+    g = torch.Generator().manual_seed(9)
+    gq, gk, gv = (torch.randn(b, h, n, d, generator=g).bfloat16() for _ in range(3))
+    x = qkv.double().requires_grad_(True)
+    q, k, v = _producer_fp64(x, qw, kw, freqs, h, d)
+    (q * gq.double()).sum().add_((k * gk.double()).sum()).add_((v * gv.double()).sum()).backward()
+    want = x.grad
+    got = O.qkv_postprocess_backward(qkv, qw, kw, freqs, gq, gk, gv, h, d)
+    assert got.shape == qkv.shape and got.dtype == torch.bfloat16
+    err = (got.double() - want).abs()
+    assert (err <= 1.01 * _ulp_bf16(want.float()).double() + 1e-9).all(), err.max()
+    # v's gradient is the incoming one, untransposed
+    assert torch.equal(got[..., 2 * h * d:], gv.movedim(1, 2).reshape(b, n, h * d))
