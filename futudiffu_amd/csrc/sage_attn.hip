@@ -8,9 +8,11 @@
 // Work decomposition: one workgroup = 4 waves = 128 query rows (the reference
 // Q tile, so a reference tile mask is workgroup-uniform); each wave owns 32
 // query rows.  Keys stream in 64-key tiles (the reference KV tile, which is
-// also the V-scale block) through a ring of three LDS stages: while tile i is
-// consumed, tile i+1 already feeds the next S^T and tile i+2 travels from
-// global memory through registers into the third stage; one barrier per tile.
+// also the V-scale block) through a ring of LDS stages filled by direct
+// global -> LDS loads: tile i+2 is issued while tile i is consumed and tile
+// i+1 already feeds the next S^T; one barrier per tile.  With fp8 P.V (int8
+// QK, per-token scales) the product of tile i-1 is formed in iteration i, its
+// MFMAs under tile i's score conversion (four stages).
 //
 // Per wave and tile:
 //   S^T[key][query] = K . Q^T with v_mfma_i32_32x32x32_i8 (int8) or
@@ -102,30 +104,30 @@ __global__ void __launch_bounds__(256) doc_summary_kernel(const int32_t* __restr
   }
 }
 
-// LDS stage layout (bytes): K codes, V operand, per-key K scales, per-key
-// additive score bias (-inf for keys past N), per-channel V scales, per-key
-// document ids.
+// LDS stage layout (bytes): K codes, V operand, then a contiguous region of
+// per-key K scales (token granularity) and per-channel V scales (fp8 P.V),
+// then per-key document ids.  Every part except the document ids arrives by
+// direct global -> LDS loads.
 template <int D, int PV>
 struct Stage {
   static constexpr int kBytes = 64 * D;
   static constexpr int vBytes = (PV == kPV_FP8 ? 64 : 128) * D;
   static constexpr int offV = kBytes;
   static constexpr int offKd = offV + vBytes;
-  static constexpr int offKb = offKd + 256;  // per-key additive bias: 0, or -inf past N
-  static constexpr int offVd = offKb + 256;
-  static constexpr int offDoc = offVd + 4 * D;
+  static constexpr int offVd = offKd + 256;
+  static constexpr int offDoc = offVd + (PV == kPV_FP8 ? 4 * D : 0);
   static constexpr int bytes = offDoc + 256;
-  // 16-byte chunks of the K|V bulk, spread over all 256 threads
-  static constexpr int cK = kBytes / 16, cV = vBytes / 16;
-  static constexpr int perThread = (cK + cV) / 256;  // 4 (D=128 fp8), 6 (D=128 bf16), 2/3 (D=64)
+  static constexpr int cK = kBytes / 16, cV = vBytes / 16;  // 16-byte chunks of the K and V parts
 };
 
-// Workgroup LDS: a ring of three stages (tile i is consumed while tile i+1
-// feeds the next QK^T and tile i+2 is being written), then a 32-float row
-// exchange per wave.  The bf16 output staging of the epilogue reuses the ring.
+// Workgroup LDS: a ring of stages, then a 32-float row exchange per wave.  With
+// bf16 P.V three stages: tile i is consumed while tile i+1 feeds the next
+// QK^T and tile i+2 is being written.  With fp8 P.V the product of tile i-1 is
+// formed while tile i is consumed, so its V stays resident one tile longer:
+// four stages.  The bf16 output staging of the epilogue reuses the ring.
 template <int D, int PV>
 struct Smem {
-  static constexpr int kStages = 3;
+  static constexpr int kStages = PV == kPV_FP8 ? 4 : 3;
   static constexpr int offX = kStages * Stage<D, PV>::bytes;
   static constexpr int bytes = offX + 4 * 32 * 4;
   static_assert(4 * 32 * D * 2 <= offX, "epilogue staging must fit in the stage ring");
@@ -158,6 +160,19 @@ __device__ __forceinline__ void item_of(int id, int total, int bh_count, int nq,
     bh = lstart + (local - hcount);
     qt = nq - 1;
   }
+}
+
+// Load at a workgroup-uniform index through the constant address space, so
+// the compiler emits a scalar load: it waits on the scalar counter, not
+// behind the stage's direct global -> LDS loads.
+__device__ __forceinline__ int4 load_uniform(const int4* base, int64_t i) {
+  typedef const __attribute__((address_space(4))) int* ConstPtr;
+  const ConstPtr q = (ConstPtr)(base + i);
+  return make_int4(q[0], q[1], q[2], q[3]);
+}
+__device__ __forceinline__ float load_uniform(const float* base, int64_t i) {
+  typedef const __attribute__((address_space(4))) float* ConstPtr;
+  return *(ConstPtr)(base + i);
 }
 
 template <int QK>
@@ -200,12 +215,23 @@ __device__ __forceinline__ void qk_both(const uint8_t* sb, const i32x4* qf, int 
   constexpr int NC = D / 32;
   const i32x4* kl = reinterpret_cast<const i32x4*>(sb);
   if constexpr (QK == kQK_INT8) {
+    // K fragments read two chunks ahead of their MFMAs: the chain waits for
+    // one LDS latency, not one per MFMA
+    i32x4 kf[2][NC];
+    auto read = [&](int c) __attribute__((always_inline)) {
+      kf[0][c] = kl[(0 * NC + c) * 64 + lane];
+      kf[1][c] = kl[(1 * NC + c) * 64 + lane];
+    };
+    read(0);
+    read(1);
     a0 = i32x16{0};
     a1 = i32x16{0};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(0 * NC + c) * 64 + lane], qf[c], a0, 0, 0, 0);
-      a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(1 * NC + c) * 64 + lane], qf[c], a1, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0][c], qf[c], a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1][c], qf[c], a1, 0, 0, 0);
+      if (c + 2 < NC) read(c + 2);
     }
   } else {
     qk_half<D, QK>(sb, qf, lane, 0, a0);
@@ -233,57 +259,62 @@ __device__ __forceinline__ void rows_of(float* xrow, float v, int h, int r, floa
   }
 }
 
-// The per-tile work of one wave, as straight-line code for the scheduler:
-// scores of tile t from s0/s1, the next tile's S^T into s0/s1 (both halves
-// issued first, as two interleaved MFMA chains, so the matrix cores overlap
-// this tile's vector work), online softmax, P.V.
-// MASKED selects the per-token document-id visibility test.
-template <int D, int QK, int PV, int GRAN, int MASK, bool MASKED>
-__device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_next, const i32x4* qf, int lane,
-                                          typename SAccT<QK>::type& s0, typename SAccT<QK>::type& s1, f32x16* o,
-                                          float& m_ref, float& l_acc, float wt, float* xrow, int dq) {
+// Scores of the 32-key half b of the tile in stage sb from its S^T
+// accumulators s: u = acc * kd (log2 units before the query scale), with kd
+// the per-key K scale (token granularity, from the stage) or the tile's block
+// scale kd_blk.  Keys at or past kvalid (the keys of the tile below N) get
+// -inf: only the ragged last tile tests.  With masked set (DOC), the
+// per-token document-id visibility: key visible iff doc[key] >= 0 and
+// (doc[q] == doc[key] or doc[q] < 0).
+template <int D, int QK, int PV, int GRAN, bool DOC>
+__device__ __forceinline__ void half_scores(const uint8_t* sb, const typename SAccT<QK>::type& s, int b, int h,
+                                            float kd_blk, int kvalid, bool masked, int dq, float (&u)[16]) {
   using St = Stage<D, PV>;
-  constexpr int NC = D / 32;
-  constexpr float kTau = 8.0f;  // lazy frame: the reference point moves when a block max exceeds it by this
-  const int h = lane >> 5, r = lane & 31;
-
-  // ---- scores of this tile: u = acc * kd + kbias (log2 units before wt) -------
-  // kd is the per-key K scale (the block scale for 64-token granularity) and
-  // kbias is -inf for keys past N, so the ragged last tile needs no test.
-  float u[2][16];
-  {
-    const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
-    const f32x4* kbl = reinterpret_cast<const f32x4*>(sb + St::offKb);
+  const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+  for (int j = 0; j < 4; ++j) {
+    f32x4 kd4;
+    if constexpr (GRAN == kGRAN_TOKEN)
+      kd4 = kdl[8 * b + 2 * j + h];
+    else
+      kd4 = f32x4{kd_blk, kd_blk, kd_blk, kd_blk};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 kd4 = kdl[8 * b + 2 * j + h];
-        const f32x4 kb4 = kbl[8 * b + 2 * j + h];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) u[b][4 * j + i] = fmaf((float)(b ? s1 : s0)[4 * j + i], kd4[i], kb4[i]);
-      }
+    for (int i = 0; i < 4; ++i) u[4 * j + i] = (float)s[4 * j + i] * kd4[i];
   }
-  qk_both<D, QK>(sb_next, qf, lane, s0, s1);
-  if constexpr (MASKED) {
-    // per-token document ids: key visible iff doc[key] >= 0 and (doc[q] == doc[key] or doc[q] < 0)
-    const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
+  if (kvalid < 64) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (32 * b + 8 * j + 4 * h + i >= kvalid) u[4 * j + i] = -INFINITY;
+  }
+  if constexpr (DOC) {
+    if (masked) {
+      const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int4 dk4 = dkl[8 * b + 2 * j + h];
         const int dk[4] = {dk4.x, dk4.y, dk4.z, dk4.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (!(dk[i] >= 0 && (dq == dk[i] || dq < 0))) u[b][4 * j + i] = -INFINITY;
+          if (!(dk[i] >= 0 && (dq == dk[i] || dq < 0))) u[4 * j + i] = -INFINITY;
       }
+    }
   }
+}
 
-  // ---- row max: max3 tree, then across the two lane halves --------------------
+// Row max of the tile's 32 scores per lane (max3 tree, then across the two
+// lane halves) in log2 units, and the lazy frame move: the reference point
+// m_ref moves to the block max bm when bm exceeds it by more than kTau, and
+// O and l are rescaled then (branch-free values, the O rescale only when some
+// row of the wave moves).  Returns bm (-inf for a row that sees no key).
+template <int D>
+__device__ __forceinline__ float row_max_move(float (&u)[2][16], float wt, float& m_ref, float& l_acc, f32x16* o,
+                                              float* xrow, int h, int r) {
+  constexpr int NC = D / 32;
+  constexpr float kTau = 8.0f;
   float mx;
   {
-    // 32 values -> 10 + 2 -> 4 -> 2 -> 1 with three-input maxima (v_max3_f32)
     auto max3 = [](float a, float b, float c) { return __builtin_fmaxf(__builtin_fmaxf(a, b), c); };
     const float* w = &u[0][0];
     float l1[12];
@@ -301,8 +332,6 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
   }
   const float bm = mx * wt;  // -inf if nothing visible in this row
   const bool row_live = bm > -INFINITY;
-
-  // ---- lazy frame move: values branch-free, the O rescale only when needed ---
   const bool move = row_live && !(bm <= m_ref + kTau);
   const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - bm) : 1.0f;  // 0 when m_ref = -inf
   m_ref = move ? bm : m_ref;
@@ -315,73 +344,117 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
 #pragma unroll
       for (int e = 0; e < 16; ++e) o[c][e] *= arow[e];
   }
+  return bm;
+}
 
-  if constexpr (PV == kPV_FP8) {
-    // reference per-(row, 64-key block) P codes: e = 2^(s - bm) * 448; the
-    // block's product is dequantized by 2^(bm - m_ref) / 448 per row and by
-    // the V scale per channel (sage_kernels.py:1137-1153)
-    const float rsc = row_live ? __builtin_amdgcn_exp2f(bm - m_ref) * (1.0f / kFp8Max) : 0.0f;
-    const float bias = row_live ? (kLog2Fp8Max - bm) : 0.0f;  // masked u are -inf: e = 0
-    float es[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    i32x8 pa;
+template <int D>
+__device__ __forceinline__ void softmax_fp8(float (&u)[2][16], float wt, float& m_ref, float& l_acc, f32x16* o,
+                                            float* xrow, int h, int r, i32x8& pa, float& rsc) {
+  const float bm = row_max_move<D>(u, wt, m_ref, l_acc, o, xrow, h, r);
+  const bool row_live = bm > -INFINITY;
+  rsc = row_live ? __builtin_amdgcn_exp2f(bm - m_ref) * (1.0f / kFp8Max) : 0.0f;
+  const float bias = row_live ? (kLog2Fp8Max - bm) : 0.0f;  // masked u are -inf: e = 0
+  float es[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+  for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float e4[4];
+    for (int j = 0; j < 4; ++j) {
+      float e4[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          e4[i] = __builtin_amdgcn_exp2f(fmaf(u[b][4 * j + i], wt, bias));
-          es[i] += e4[i];
-        }
-        pa[4 * b + j] = (int)pack_fp8x4(e4[0], e4[1], e4[2], e4[3]);
+      for (int i = 0; i < 4; ++i) {
+        e4[i] = __builtin_amdgcn_exp2f(fmaf(u[b][4 * j + i], wt, bias));
+        es[i] += e4[i];
       }
-    l_acc = fmaf(rsc, (es[0] + es[1]) + (es[2] + es[3]), l_acc);
-    const i32x4* vl = reinterpret_cast<const i32x4*>(sb + St::offV);
-    const float* vdl = reinterpret_cast<const float*>(sb + St::offVd);
-    auto pv = [&](int c) {
-      const i32x4 b0 = vl[(c * 2 + 0) * 64 + lane], b1 = vl[(c * 2 + 1) * 64 + lane];
-      const i32x8 bv = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-      return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(pa, bv, f32x16{0}, 0, 0, 0, 0, 0, 0);
-    };
-    // The per-element factors rsc[row] * vd[channel] are rank-1 products, made
-    // on the matrix cores already in the O layout: v_mfma_f32_32x32x1_2b_f32
-    // forms two 32x32 outer products, block b from the lanes h = b, with A =
-    // rsc of query r (lane-local in the S^T layout) and B = the V scale of
-    // channel 32(c2 + b) + r.  Each product is one correctly rounded fp32
-    // multiply, as on the vector ALU, and no lane exchange is needed.
+      pa[4 * b + j] = (int)pack_fp8x4(e4[0], e4[1], e4[2], e4[3]);
+    }
+  l_acc = fmaf(rsc, (es[0] + es[1]) + (es[2] + es[3]), l_acc);
+}
+
+// fp8 P.V of one tile for the chunk pair (c2, c2 + 1): the block products
+// p0, p1 (v_mfma_f32_32x32x64_f8f6f4, P codes pa against the V codes of stage
+// sb) and their dequantization factors rsc[row] * vd[channel] in the O layout.
+// The factors are rank-1 products made on the matrix cores:
+// v_mfma_f32_32x32x1_2b_f32 forms two 32x32 outer products, block b from the
+// lanes h = b, with A = rsc of query r (lane-local in the S^T layout) and B =
+// the V scale of channel 32(c2 + b) + r; each product is one correctly
+// rounded fp32 multiply, as on the vector ALU, and no lane exchange is needed.
+template <int D>
+__device__ __forceinline__ void pv_issue(const uint8_t* sb, const i32x8& pa, float rsc, int lane, int c2, f32x16& p0,
+                                         f32x16& p1, f32x32& rv) {
+  using St = Stage<D, kPV_FP8>;
+  const int h = lane >> 5, r = lane & 31;
+  const i32x4* vl = reinterpret_cast<const i32x4*>(sb + St::offV);
+  const float* vdl = reinterpret_cast<const float*>(sb + St::offVd);
+  rv = __builtin_amdgcn_mfma_f32_32x32x1f32(rsc, vdl[32 * (c2 + h) + r], f32x32{0}, 0, 0, 0);
+  auto pv = [&](int c) {
+    const i32x4 b0 = vl[(c * 2 + 0) * 64 + lane], b1 = vl[(c * 2 + 1) * 64 + lane];
+    const i32x8 bv = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(pa, bv, f32x16{0}, 0, 0, 0, 0, 0, 0);
+  };
+  p0 = pv(c2);
+  p1 = pv(c2 + 1);
+}
+
+__device__ __forceinline__ void pv_accum(f32x16* o, int c2, const f32x16& p0, const f32x16& p1, const f32x32& rv) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) o[c2][e] = fmaf(p0[e], rv[e], o[c2][e]);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) o[c2 + 1][e] = fmaf(p1[e], rv[16 + e], o[c2 + 1][e]);
+}
+
+// The per-tile work of one wave in the general loop, as straight-line code
+// for the scheduler: scores of tile t from s0/s1, the next tile's S^T into
+// s0/s1 (both halves issued first, as two interleaved MFMA chains, so the
+// matrix cores overlap this tile's vector work), online softmax, then P.V:
+// bf16 accumulated straight into O, or fp8 dequantized into O right away.
+// MASKED selects the per-token document-id visibility test.
+template <int D, int QK, int PV, int GRAN, int MASK, bool MASKED>
+__device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_next, const i32x4* qf, int lane,
+                                          typename SAccT<QK>::type& s0, typename SAccT<QK>::type& s1, f32x16* o,
+                                          float& m_ref, float& l_acc, float wt, float* xrow, int dq, float kd_blk,
+                                          int kvalid) {
+  using St = Stage<D, PV>;
+  constexpr int NC = D / 32;
+  const int h = lane >> 5, r = lane & 31;
+  float u[2][16];
+  half_scores<D, QK, PV, GRAN, MASKED>(sb, s0, 0, h, kd_blk, kvalid, true, dq, u[0]);
+  half_scores<D, QK, PV, GRAN, MASKED>(sb, s1, 1, h, kd_blk, kvalid, true, dq, u[1]);
+  qk_both<D, QK>(sb_next, qf, lane, s0, s1);
+  if constexpr (PV == kPV_FP8) {
+    i32x8 pa;
+    float rsc;
+    softmax_fp8<D>(u, wt, m_ref, l_acc, o, xrow, h, r, pa, rsc);
 #pragma unroll
     for (int c2 = 0; c2 < NC; c2 += 2) {
-      const f32x32 rv = __builtin_amdgcn_mfma_f32_32x32x1f32(rsc, vdl[32 * (c2 + h) + r], f32x32{0}, 0, 0, 0);
-      const f32x16 p0 = pv(c2), p1 = pv(c2 + 1);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[c2][e] = fmaf(p0[e], rv[e], o[c2][e]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[c2 + 1][e] = fmaf(p1[e], rv[16 + e], o[c2 + 1][e]);
+      f32x16 p0, p1;
+      f32x32 rv;
+      pv_issue<D>(sb, pa, rsc, lane, c2, p0, p1, rv);
+      pv_accum(o, c2, p0, p1, rv);
     }
-  } else {
-    // bf16 P = 2^(s - m_ref) <= 2^kTau, accumulated straight into O
-    const float bias = row_live ? -m_ref : 0.0f;
-    float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    bf16x8 pa[2][2];
+    return;
+  }
+  const float bm = row_max_move<D>(u, wt, m_ref, l_acc, o, xrow, h, r);
+  // bf16 P = 2^(s - m_ref) <= 2^kTau, accumulated straight into O
+  const float bias = bm > -INFINITY ? -m_ref : 0.0f;
+  float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  bf16x8 pa[2][2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pr = __builtin_amdgcn_exp2f(fmaf(u[b][e], wt, bias));
+      ls[e & 3] += pr;
+      pa[b][e >> 3][e & 7] = (__bf16)pr;
+    }
+  l_acc += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+  const bf16x8* vl = reinterpret_cast<const bf16x8*>(sb + St::offV);
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pr = __builtin_amdgcn_exp2f(fmaf(u[b][e], wt, bias));
-        ls[e & 3] += pr;
-        pa[b][e >> 3][e & 7] = (__bf16)pr;
-      }
-    l_acc += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-    const bf16x8* vl = reinterpret_cast<const bf16x8*>(sb + St::offV);
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-          o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[b][tt], vl[((c * 2 + b) * 2 + tt) * 64 + lane], o[c], 0, 0, 0);
-  }
+      for (int tt = 0; tt < 2; ++tt)
+        o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[b][tt], vl[((c * 2 + b) * 2 + tt) * 64 + lane], o[c], 0, 0, 0);
 }
 
 // Tiles [t_begin, t_end) of work item (bh, query tile qt) for this wave:
@@ -396,7 +469,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
   using SAcc = typename SAccT<QK>::type;
   constexpr int NC = D / 32;  // 32-channel chunks
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int r = lane & 31;
+  const int h = lane >> 5, r = lane & 31;
   const int nq = (int)(p.np / kRowsPerWG);
   const int bidx = bh / p.h;
   const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * wave;  // first query row of this wave
@@ -442,123 +515,215 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
         if (p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] == 0) continue;
       }
       if (MASK & 2) {
-        if (classify(qsum128, p.kv_sum[(int64_t)bidx * p.nt + t]) == 0) continue;
+        if (classify(qsum128, load_uniform(p.kv_sum, (int64_t)bidx * p.nt + t)) == 0) continue;
       }
       break;
     }
     return t;
   };
 
-  // ---- loads: global -> registers -> LDS stage ---------------------------------
-  // Thread tid moves 16-byte chunks tid + 256*i of the stage's K|V bulk, and
-  // threads 0..63 one small chunk: K scales and score biases (0..15), V scales
-  // (16..16+D/4), key document ids (48..63).
-  static_assert(St::perThread <= 6 && St::cK % 256 == 0, "stage chunking");
-  uint4 pre0, pre1, pre2, pre3, pre4, pre5;  // scalars: an indexed array would live in scratch
-  uint4 pre_small = make_uint4(0, 0, 0, 0), pre_bias = make_uint4(0, 0, 0, 0);
-#define SAGE_CHUNK_LD(I_, DST_)                                                                        \
-  if constexpr (St::perThread > I_) DST_ = (256 * I_ < St::cK) ? ksrc_[tid + 256 * I_] : vsrc_[tid + 256 * I_ - St::cK]
-#define SAGE_CHUNK_ST(I_, SRC_) \
-  if constexpr (St::perThread > I_) reinterpret_cast<uint4*>(sb_)[tid + 256 * I_] = SRC_
-#define SAGE_LOAD_TILE(T_)                                                                             \
-  do {                                                                                                 \
-    const uint4* ksrc_ = reinterpret_cast<const uint4*>(kg + (int64_t)(T_) * 64 * D);                  \
-    const uint4* vsrc_ = reinterpret_cast<const uint4*>(vg + (int64_t)(T_) * St::vBytes);              \
-    const uint32_t kdb_ = GRAN == kGRAN_TOKEN ? 0u : __float_as_uint(p.ks[(int64_t)bh * (p.np / 64) + (T_)]); \
-    SAGE_CHUNK_LD(0, pre0);                                                                            \
-    SAGE_CHUNK_LD(1, pre1);                                                                            \
-    SAGE_CHUNK_LD(2, pre2);                                                                            \
-    SAGE_CHUNK_LD(3, pre3);                                                                            \
-    SAGE_CHUNK_LD(4, pre4);                                                                            \
-    SAGE_CHUNK_LD(5, pre5);                                                                            \
-    if (tid < 16) {                                                                                    \
-      if (GRAN == kGRAN_TOKEN)                                                                         \
-        pre_small = reinterpret_cast<const uint4*>(p.ks + (int64_t)bh * p.np + (int64_t)(T_) * 64)[tid]; \
-      else                                                                                             \
-        pre_small = make_uint4(kdb_, kdb_, kdb_, kdb_);                                                \
-      const int key_ = (T_) * 64 + 4 * tid;                                                            \
-      const uint32_t ninf_ = 0xff800000u;                                                              \
-      pre_bias = make_uint4(key_ + 0 < p.n ? 0u : ninf_, key_ + 1 < p.n ? 0u : ninf_,                  \
-                            key_ + 2 < p.n ? 0u : ninf_, key_ + 3 < p.n ? 0u : ninf_);                 \
-    } else if (tid < 16 + D / 4) {                                                                     \
-      if (PV == kPV_FP8)                                                                               \
-        pre_small = reinterpret_cast<const uint4*>(p.vs + ((int64_t)bh * (p.np / 64) + (T_)) * D)[tid - 16]; \
-    } else if ((MASK & 2) && tid >= 48 && tid < 64) {                                                  \
-      const int64_t base_ = (int64_t)(T_) * 64 + (tid - 48) * 4;                                       \
-      pre_small.x = (uint32_t)(base_ + 0 < p.n ? docb[base_ + 0] : -1);                                \
-      pre_small.y = (uint32_t)(base_ + 1 < p.n ? docb[base_ + 1] : -1);                                \
-      pre_small.z = (uint32_t)(base_ + 2 < p.n ? docb[base_ + 2] : -1);                                \
-      pre_small.w = (uint32_t)(base_ + 3 < p.n ? docb[base_ + 3] : -1);                                \
-    }                                                                                                  \
-  } while (0)
-#define SAGE_STORE_TILE(STAGE_)                                                                        \
-  do {                                                                                                 \
-    uint8_t* sb_ = smem + (STAGE_) * St::bytes;                                                        \
-    SAGE_CHUNK_ST(0, pre0);                                                                            \
-    SAGE_CHUNK_ST(1, pre1);                                                                            \
-    SAGE_CHUNK_ST(2, pre2);                                                                            \
-    SAGE_CHUNK_ST(3, pre3);                                                                            \
-    SAGE_CHUNK_ST(4, pre4);                                                                            \
-    SAGE_CHUNK_ST(5, pre5);                                                                            \
-    if (tid < 16) {                                                                                    \
-      reinterpret_cast<uint4*>(sb_ + St::offKd)[tid] = pre_small;                                      \
-      reinterpret_cast<uint4*>(sb_ + St::offKb)[tid] = pre_bias;                                       \
-    } else if (tid < 16 + D / 4) {                                                                     \
-      if (PV == kPV_FP8) reinterpret_cast<uint4*>(sb_ + St::offVd)[tid - 16] = pre_small;              \
-    } else if ((MASK & 2) && tid >= 48 && tid < 64) {                                                  \
-      reinterpret_cast<uint4*>(sb_ + St::offDoc)[tid - 48] = pre_small;                                \
-    }                                                                                                  \
-  } while (0)
+  // ---- loads: global -> LDS stage --------------------------------------------
+  // The K and V parts in 64-chunk blocks spread over the four waves, the K and
+  // V scales by lanes of wave 0, all as direct global -> LDS loads; the key
+  // document ids (bounds-checked: -1 past N) through registers of threads
+  // 48..63.  The caller waits for vmcnt(0) before the barrier that publishes
+  // the stage.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  int4 pre_doc = make_int4(-1, -1, -1, -1);
+  auto load_tile = [&](int tt, uint8_t* sbw) __attribute__((always_inline)) {
+    const uint8_t* ksrc = kg + (int64_t)tt * 64 * D;
+    const uint8_t* vsrc = vg + (int64_t)tt * St::vBytes;
+    // uniform base + 32-bit lane offset: the scalar-base addressing form
+    dma_chunks<St::cK, 4>(sbw, wave_u, lane, [&](int x) { return ksrc + (uint32_t)(x * 16); });
+    dma_chunks<St::cV, 4>(sbw + St::offV, wave_u, lane, [&](int x) { return vsrc + (uint32_t)(x * 16); });
+    if (wave_u == 0) {
+      const bool kd_lane = GRAN == kGRAN_TOKEN && lane < 16;
+      const bool vd_lane = PV == kPV_FP8 && lane >= 16 && lane < 16 + D / 4;
+      if (kd_lane || vd_lane) {
+        const uint8_t* src =
+            kd_lane ? reinterpret_cast<const uint8_t*>(p.ks + (int64_t)bh * p.np + (int64_t)tt * 64) + (uint32_t)(lane * 16)
+                    : reinterpret_cast<const uint8_t*>(p.vs + ((int64_t)bh * (p.np / 64) + tt) * D) +
+                          (uint32_t)((lane - 16) * 16);
+        __builtin_amdgcn_global_load_lds(src, sbw + St::offKd, 16, 0, 0);
+      }
+    }
+    if ((MASK & 2) && tid >= 48 && tid < 64) {
+      const int64_t base = (int64_t)tt * 64 + (tid - 48) * 4;
+      pre_doc.x = base + 0 < p.n ? docb[base + 0] : -1;
+      pre_doc.y = base + 1 < p.n ? docb[base + 1] : -1;
+      pre_doc.z = base + 2 < p.n ? docb[base + 2] : -1;
+      pre_doc.w = base + 3 < p.n ? docb[base + 3] : -1;
+    }
+  };
+  auto store_doc = [&](uint8_t* sbw) __attribute__((always_inline)) {
+    if ((MASK & 2) && tid >= 48 && tid < 64) reinterpret_cast<int4*>(sbw + St::offDoc)[tid - 48] = pre_doc;
+  };
+  auto kd_block = [&](int tt) -> float {
+    return GRAN == kGRAN_TOKEN ? 0.0f : load_uniform(p.ks, (int64_t)bh * (p.np / 64) + tt);
+  };
+  auto keys_valid = [&](int tt) -> int { return p.n - (int64_t)tt * 64 < 64 ? (int)(p.n - (int64_t)tt * 64) : 64; };
 
   // ---- prologue: tiles 0 and 1 of the schedule in stages 0 and 1 --------------
   int t = next_active(t_begin);
   int t1 = t < t_end ? next_active(t + 1) : t_end;
   int t2 = t1 < t_end ? next_active(t1 + 1) : t_end;
   if (t < t_end) {
-    SAGE_LOAD_TILE(t);
-    SAGE_STORE_TILE(0);
+    load_tile(t, smem);
+    store_doc(smem);
   }
   if (t1 < t_end) {
-    SAGE_LOAD_TILE(t1);
-    SAGE_STORE_TILE(1);
+    load_tile(t1, smem + St::bytes);
+    store_doc(smem + St::bytes);
   }
+  wait_vmem();
   __syncthreads();
   SAcc s0, s1;  // S^T of the tile about to be consumed
   if (t < t_end && wave_live) {
     qk_both<D, QK>(smem, qf, lane, s0, s1);
   }
 
+  constexpr int kSt = SM::kStages;
+  // (Taken where its registers fit without spilling: the other fp8 P.V
+  // variants run the general loop below.)
+  constexpr bool kFast = PV == kPV_FP8 && (MASK & 2) == 0 && ((QK == kQK_INT8 && GRAN == kGRAN_TOKEN) || D == 64);
+  if constexpr (kFast) {
+    // ---- fp8 P.V, no per-token visibility: every scheduled tile is computed by
+    // every live wave, so the product of tile i-1 is always pending in
+    // iteration i.  The first and the last tile are peeled off the loop, which
+    // leaves its body one straight basic block for the scheduler: the pending
+    // P.V in two chunk-pair halves, each under half of this tile's score
+    // conversion, then the next tile's S^T under this tile's softmax.
+    constexpr int NP = NC / 2;
+    int stage = 0;
+    auto sp = [&](int s_) { return smem + s_ * St::bytes; };
+    auto next_stage = [&](int s_, int k_) { return (s_ + k_) % kSt; };
+    auto advance = [&]() __attribute__((always_inline)) {
+      stage = next_stage(stage, 1);
+      t = t1;
+      t1 = t2;
+      t2 = t2 < t_end ? next_active(t2 + 1) : t_end;
+    };
+    auto publish = [&]() __attribute__((always_inline)) {
+      wait_vmem();
+      __syncthreads();
+    };
+    if (!wave_live) {
+      // rows past N: the same loads and barriers, nothing computed
+      while (t < t_end) {
+        if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+        publish();
+        advance();
+      }
+      __syncthreads();
+      return;
+    }
+    const bool any = t < t_end;
+    i32x8 pa_p = {0, 0, 0, 0, 0, 0, 0, 0};
+    float rsc_p = 0.0f;
+    int stage_p = 0;
+    float u[2][16];
+    if (t < t_end) {  // first tile: nothing pending
+      if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+      const float kdb = kd_block(t);
+      const int kvalid = keys_valid(t);
+      half_scores<D, QK, PV, GRAN, false>(sp(stage), s0, 0, h, kdb, kvalid, false, dq, u[0]);
+      half_scores<D, QK, PV, GRAN, false>(sp(stage), s1, 1, h, kdb, kvalid, false, dq, u[1]);
+      if (t1 < t_end) qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
+      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
+      stage_p = stage;
+      publish();
+      advance();
+    }
+    while (t1 < t_end) {  // tile t is whole (a later tile exists) and has a successor
+      if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+      const uint8_t* sb = sp(stage);
+      const uint8_t* sbp = sp(stage_p);
+      const float kdb = kd_block(t);
+      f32x16 p0, p1;
+      f32x32 rv;
+      pv_issue<D>(sbp, pa_p, rsc_p, lane, 0, p0, p1, rv);
+      half_scores<D, QK, PV, GRAN, false>(sb, s0, 0, h, kdb, 64, false, dq, u[0]);
+      if constexpr (NP == 1) half_scores<D, QK, PV, GRAN, false>(sb, s1, 1, h, kdb, 64, false, dq, u[1]);
+      pv_accum(o, 0, p0, p1, rv);
+      if constexpr (NP == 2) {
+        pv_issue<D>(sbp, pa_p, rsc_p, lane, 2, p0, p1, rv);
+        half_scores<D, QK, PV, GRAN, false>(sb, s1, 1, h, kdb, 64, false, dq, u[1]);
+        pv_accum(o, 2, p0, p1, rv);
+      }
+      qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
+      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
+      stage_p = stage;
+      publish();
+      advance();
+    }
+    if (t < t_end) {  // last tile: possibly ragged, no successor
+      const uint8_t* sb = sp(stage);
+      const uint8_t* sbp = sp(stage_p);
+      const float kdb = kd_block(t);
+      const int kvalid = keys_valid(t);
+#pragma unroll
+      for (int c2 = 0; c2 < NC; c2 += 2) {
+        f32x16 p0, p1;
+        f32x32 rv;
+        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
+        pv_accum(o, c2, p0, p1, rv);
+        __builtin_amdgcn_sched_barrier(0);  // one pair's products in flight at a time
+      }
+      half_scores<D, QK, PV, GRAN, false>(sb, s0, 0, h, kdb, kvalid, false, dq, u[0]);
+      half_scores<D, QK, PV, GRAN, false>(sb, s1, 1, h, kdb, kvalid, false, dq, u[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
+      stage_p = stage;
+      publish();
+      advance();
+    }
+    if (any) {  // the last tile's P.V
+      const uint8_t* sbp = sp(stage_p);
+#pragma unroll
+      for (int c2 = 0; c2 < NC; c2 += 2) {
+        f32x16 p0, p1;
+        f32x32 rv;
+        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
+        pv_accum(o, c2, p0, p1, rv);
+        __builtin_amdgcn_sched_barrier(0);  // one pair's products in flight at a time
+      }
+    }
+    __syncthreads();  // the ring is reused after
+  } else {
   int stage = 0;
   while (t < t_end) {
-    if (t2 < t_end) SAGE_LOAD_TILE(t2);
     const uint8_t* sb = smem + stage * St::bytes;
-    const int stage1 = stage == 2 ? 0 : stage + 1;
-    const int stage2 = stage1 == 2 ? 0 : stage1 + 1;
-    // the last tile recomputes its own S^T in place of a next tile's (unused)
-    const uint8_t* sb_next = t1 < t_end ? smem + stage1 * St::bytes : sb;
+    const int stage1 = stage + 1 == kSt ? 0 : stage + 1;
+    const int stage2 = stage1 + 1 == kSt ? 0 : stage1 + 1;
+    // tile t2 into a stage no wave reads any more (the last barrier ended
+    // every read of it)
+    if (t2 < t_end) load_tile(t2, smem + stage2 * St::bytes);
+    const float kdb = kd_block(t);
+    const int kvalid = keys_valid(t);
 
     int cls = wave_live ? 1 : 0;
-    if ((MASK & 2) && cls) cls = classify(qsum, p.kv_sum[(int64_t)bidx * p.nt + t]);
+    if ((MASK & 2) && cls) cls = classify(qsum, load_uniform(p.kv_sum, (int64_t)bidx * p.nt + t));
+    // the last tile recomputes its own S^T in place of a next tile's (unused)
+    const uint8_t* sb_next = t1 < t_end ? smem + stage1 * St::bytes : sb;
     if (cls == 2)
-      tile_body<D, QK, PV, GRAN, MASK, true>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq);
+      tile_body<D, QK, PV, GRAN, MASK, true>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kdb,
+                                             kvalid);
     else if (cls == 1)
-      tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq);
-    else if (wave_live && t1 < t_end) {
+      tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kdb,
+                                              kvalid);
+    else if (wave_live && t1 < t_end)
       qk_both<D, QK>(sb_next, qf, lane, s0, s1);
-    }
 
-    // ---- hand over: tile t2 into the stage tile t - 1 used ----------------------
-    if (t2 < t_end) SAGE_STORE_TILE(stage2);
+    // ---- publish tile t2 ---------------------------------------------------------
+    if (t2 < t_end) store_doc(smem + stage2 * St::bytes);
+    wait_vmem();
     __syncthreads();
     stage = stage1;
     t = t1;
     t1 = t2;
     t2 = t2 < t_end ? next_active(t2 + 1) : t_end;
   }
-#undef SAGE_LOAD_TILE
-#undef SAGE_STORE_TILE
-#undef SAGE_CHUNK_LD
-#undef SAGE_CHUNK_ST
+  }
 }
 
 constexpr int kRawBufferWord3 = 0x00020000;  // word 3 of a raw (untyped) buffer resource, gfx9 family
