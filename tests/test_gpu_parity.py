@@ -149,6 +149,12 @@ ATTN_CASES = [
     (2, 2, 200, 128, "int8", "fp8", "token"),
     (1, 3, 77, 64, "fp8", "bf16", "token"),
     (1, 2, 1, 128, "int8", "fp8", "token"),
+    # single whole tile; D = 64 with fp8 P.V (software-pipelined loop, one
+    # chunk pair) and the general loop's fp8 QK / block-scale variant
+    (1, 2, 64, 128, "int8", "fp8", "token"),
+    (1, 3, 77, 64, "int8", "fp8", "token"),
+    (2, 2, 300, 64, "int8", "fp8", "token"),
+    (1, 2, 300, 64, "fp8", "fp8", "block64"),
 ]
 
 
@@ -264,7 +270,7 @@ def test_headline_schedule_consistency(cuda, qk, pv):
     assert (la - lb).abs().max().item() <= 1e-4
 
 
-@pytest.mark.parametrize("qk,pv,D", [("int8", "fp8", 128), ("fp8", "bf16", 64)])
+@pytest.mark.parametrize("qk,pv,D", [("int8", "fp8", 128), ("fp8", "bf16", 64), ("int8", "fp8", 64)])
 def test_split_tail_matches_oracle(cuda, qk, pv, D):
     """520 query-tile items (2 x 130 heads x 2 tiles) fill one round of 512
     workgroups and leave 8 items that are cut into 4 key-tile pieces each and
