@@ -162,19 +162,6 @@ __device__ __forceinline__ void item_of(int id, int total, int bh_count, int nq,
   }
 }
 
-// Load at a workgroup-uniform index through the constant address space, so
-// the compiler emits a scalar load: it waits on the scalar counter, not
-// behind the stage's direct global -> LDS loads.
-__device__ __forceinline__ int4 load_uniform(const int4* base, int64_t i) {
-  typedef const __attribute__((address_space(4))) int* ConstPtr;
-  const ConstPtr q = (ConstPtr)(base + i);
-  return make_int4(q[0], q[1], q[2], q[3]);
-}
-__device__ __forceinline__ float load_uniform(const float* base, int64_t i) {
-  typedef const __attribute__((address_space(4))) float* ConstPtr;
-  return *(ConstPtr)(base + i);
-}
-
 template <int QK>
 struct SAccT {
   using type = f32x16;

@@ -253,7 +253,8 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
   constexpr int NC = D / 32, CPR = D / 8;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * St::bytes];
   static_assert(4 * NC * 16 * 64 * 4 <= 2 * St::bytes, "partial dQ exchange must fit in the ring");
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int h = lane >> 5, r = lane & 31;
   const int qg = wave & 3, b = wave >> 2;  // query group, key half
   const int nq = (int)(p.np / kRowsPerWG);
@@ -298,8 +299,9 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
   }
   auto active = [&](int t) __attribute__((always_inline)) -> bool {
     bool on = true;
-    if constexpr (MASK & 1) on = p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] != 0;
-    if constexpr (MASK & 2) on = on && classify(qsum128, p.kv_sum[(int64_t)bidx * nt + t]) != 0;
+    if constexpr (MASK & 1)
+      on = load_uniform_u8(p.tile_mask, (int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t) != 0;
+    if constexpr (MASK & 2) on = on && classify(qsum128, load_uniform(p.kv_sum, (int64_t)bidx * nt + t)) != 0;
     return on;
   };
   auto next_active = [&](int t) __attribute__((always_inline)) -> int {
@@ -315,9 +317,9 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
     const uint8_t* kcs = p.kc + ((int64_t)bh * np + key0) * D;
     const uint8_t* tks = reinterpret_cast<const uint8_t*>(p.tk + ((int64_t)bh * np + key0) * D);
     const uint8_t* rvs = reinterpret_cast<const uint8_t*>(p.rv + ((int64_t)bh * np + key0) * D);
-    dma_chunks<St::cKc>(sb, wave, lane, [&](int x) { return kcs + x * 16; });
-    dma_chunks<St::cRow>(sb + St::offT, wave, lane, [&](int x) { return tks + x * 16; });
-    dma_chunks<St::cRow>(sb + St::offV, wave, lane, [&](int x) { return rvs + x * 16; });
+    dma_chunks<St::cKc>(sb, wave, lane, [&](int x) { return kcs + (uint32_t)(x * 16); });
+    dma_chunks<St::cRow>(sb + St::offT, wave, lane, [&](int x) { return tks + (uint32_t)(x * 16); });
+    dma_chunks<St::cRow>(sb + St::offV, wave, lane, [&](int x) { return rvs + (uint32_t)(x * 16); });
     if (tid < 16) {
       psm = reinterpret_cast<const u32x4*>(p.ks + (int64_t)bh * np + key0)[tid];
     } else if ((MASK & 2) && tid < 32) {
@@ -347,7 +349,8 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
     const int tn = next_active(t + 1);
     if (tn < nt) load_tile(tn, stage ^ 1);
     bool wave_on = wave_live;
-    if constexpr (MASK & 2) wave_on = wave_on && classify(qsum32, p.kv_sum[(int64_t)bidx * nt + t]) != 0;
+    if constexpr (MASK & 2)
+      wave_on = wave_on && classify(qsum32, load_uniform(p.kv_sum, (int64_t)bidx * nt + t)) != 0;
     if (wave_on) {
       const uint8_t* sb = smem + stage * St::bytes;
       // S^T = K . Q^T for keys 32b + (lane-local rows) x this wave's queries
@@ -481,7 +484,8 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
   constexpr int kVOff = 2 * St::bytes;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kVOff + kRowsPerWG * 2 * D];
   static_assert(4 * NC * 16 * 64 * 4 <= 2 * St::bytes, "partial dK/dV exchange must fit in the ring");
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int h = lane >> 5, r = lane & 31;
   const int kg = wave & 3, a = wave >> 2;  // key group, query half
   const int nkb = (int)(p.np / kRowsPerWG);
@@ -506,7 +510,7 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
   {
     // the R image of V rows [kb*128, +128) into the persistent region
     const uint8_t* rvs = reinterpret_cast<const uint8_t*>(p.rv + ((int64_t)bh * np + (int64_t)kb * kRowsPerWG) * D);
-    dma_chunks<kRowsPerWG * CPR>(smem + kVOff, wave, lane, [&](int x) { return rvs + x * 16; });
+    dma_chunks<kRowsPerWG * CPR>(smem + kVOff, wave, lane, [&](int x) { return rvs + (uint32_t)(x * 16); });
   }
   const u32x4* vrl = reinterpret_cast<const u32x4*>(smem + kVOff);
   const float kd = p.ks[(int64_t)bh * np + krow];
@@ -526,22 +530,23 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
   if constexpr (MASK & 2) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      ksum[i] = 2 * kb + i < nkv ? p.kv_sum[(int64_t)bidx * nkv + 2 * kb + i] : make_int4(0x7fffffff, -0x7fffffff, 0, 0);
+      ksum[i] = 2 * kb + i < nkv ? load_uniform(p.kv_sum, (int64_t)bidx * nkv + 2 * kb + i)
+                                 : make_int4(0x7fffffff, -0x7fffffff, 0, 0);
   }
   auto wave_active = [&](int s) __attribute__((always_inline)) -> bool {
     bool on = true;
-    if constexpr (MASK & 1) on = my_tile < nkv && mrow[(int64_t)(s >> 1) * p.mask_nkv + my_tile] != 0;
-    if constexpr (MASK & 2) on = on && classify(qs32[2 * s + a], ksum[kg >> 1]) != 0;
+    if constexpr (MASK & 1) on = my_tile < nkv && load_uniform_u8(mrow, (int64_t)(s >> 1) * p.mask_nkv + my_tile) != 0;
+    if constexpr (MASK & 2) on = on && classify(load_uniform(qs32, 2 * s + a), ksum[kg >> 1]) != 0;
     return on;
   };
   auto active = [&](int s) __attribute__((always_inline)) -> bool {
     bool on = true;
     if constexpr (MASK & 1) {
       const uint8_t* m = mrow + (int64_t)(s >> 1) * p.mask_nkv;
-      on = m[2 * kb] != 0 || (2 * kb + 1 < nkv && m[2 * kb + 1] != 0);
+      on = load_uniform_u8(m, 2 * kb) != 0 || (2 * kb + 1 < nkv && load_uniform_u8(m, 2 * kb + 1) != 0);
     }
     if constexpr (MASK & 2) {
-      const int4 q64 = merge_summary(qs32[2 * s], qs32[2 * s + 1]);
+      const int4 q64 = merge_summary(load_uniform(qs32, 2 * s), load_uniform(qs32, 2 * s + 1));
       on = on && (classify(q64, ksum[0]) != 0 || classify(q64, ksum[1]) != 0);
     }
     return on;
@@ -560,10 +565,10 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
     const uint8_t* tds = reinterpret_cast<const uint8_t*>(p.tdo + ((int64_t)bh * np + m0) * D);
     const uint8_t* tqs = reinterpret_cast<const uint8_t*>(p.tq + ((int64_t)bh * np + m0) * D);
     const uint8_t* rds = reinterpret_cast<const uint8_t*>(p.rdo + ((int64_t)bh * np + m0) * D);
-    dma_chunks<St::cQc>(sb, wave, lane, [&](int x) { return qcs + x * 16; });
-    dma_chunks<St::cRow>(sb + St::offTdo, wave, lane, [&](int x) { return tds + x * 16; });
-    dma_chunks<St::cRow>(sb + St::offTq, wave, lane, [&](int x) { return tqs + x * 16; });
-    dma_chunks<St::cRow>(sb + St::offDo, wave, lane, [&](int x) { return rds + x * 16; });
+    dma_chunks<St::cQc>(sb, wave, lane, [&](int x) { return qcs + (uint32_t)(x * 16); });
+    dma_chunks<St::cRow>(sb + St::offTdo, wave, lane, [&](int x) { return tds + (uint32_t)(x * 16); });
+    dma_chunks<St::cRow>(sb + St::offTq, wave, lane, [&](int x) { return tqs + (uint32_t)(x * 16); });
+    dma_chunks<St::cRow>(sb + St::offDo, wave, lane, [&](int x) { return rds + (uint32_t)(x * 16); });
     if (tid < 16) {
       psm = reinterpret_cast<const u32x4*>(p.qs + (int64_t)bh * np + m0)[tid];
     } else if (tid < 32) {

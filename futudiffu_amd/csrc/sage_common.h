@@ -92,6 +92,27 @@ __device__ __forceinline__ void dma_chunks(uint8_t* lds, int wave, int lane, Src
   }
 }
 
+// Loads at a workgroup-uniform index through the constant address space, so
+// the compiler emits scalar loads: they wait on the scalar counter, not behind
+// direct global -> LDS loads in flight (which a vector load's vmcnt wait would
+// include).
+__device__ __forceinline__ int4 load_uniform(const int4* base, int64_t i) {
+  typedef const __attribute__((address_space(4))) int* ConstPtr;
+  const ConstPtr q = (ConstPtr)(base + i);
+  return make_int4(q[0], q[1], q[2], q[3]);
+}
+__device__ __forceinline__ float load_uniform(const float* base, int64_t i) {
+  typedef const __attribute__((address_space(4))) float* ConstPtr;
+  return *(ConstPtr)(base + i);
+}
+// Byte i of a uniform byte array, from the aligned dword that holds it.
+__device__ __forceinline__ uint32_t load_uniform_u8(const uint8_t* base, int64_t i) {
+  typedef const __attribute__((address_space(4))) uint32_t* ConstPtr;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(base + i);
+  const uint32_t w = *(ConstPtr)(a & ~(uintptr_t)3);
+  return (w >> (8 * (a & 3))) & 0xffu;
+}
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left free; gfx9 encoding).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
