@@ -499,7 +499,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
   auto next_active = [&](int t) -> int {
     for (; t < t_end; ++t) {
       if (MASK & 1) {
-        if (p.tile_mask[(int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t] == 0) continue;
+        if (load_uniform_u8(p.tile_mask, (int64_t)bh * p.mask_stride_z + (int64_t)qt * p.mask_nkv + t) == 0) continue;
       }
       if (MASK & 2) {
         if (classify(qsum128, load_uniform(p.kv_sum, (int64_t)bidx * p.nt + t)) == 0) continue;
