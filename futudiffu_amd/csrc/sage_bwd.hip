@@ -317,17 +317,25 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
     const uint8_t* kcs = p.kc + ((int64_t)bh * np + key0) * D;
     const uint8_t* tks = reinterpret_cast<const uint8_t*>(p.tk + ((int64_t)bh * np + key0) * D);
     const uint8_t* rvs = reinterpret_cast<const uint8_t*>(p.rv + ((int64_t)bh * np + key0) * D);
+    if (tid < 32) {
+      // one path for lanes 0..31 (see the dK/dV kernel): K scales (g=0),
+      // key document ids (g=1, -1 past N)
+      const int g = tid >> 4;
+      const int64_t k = key0 + 4 * (tid & 15);
+      const uint32_t* base = g == 0 ? reinterpret_cast<const uint32_t*>(p.ks + (int64_t)bh * np)
+                             : (MASK & 2) ? reinterpret_cast<const uint32_t*>(p.doc + (int64_t)bidx * n)
+                                          : reinterpret_cast<const uint32_t*>(p.ks);  // not read
+      const int64_t lim = g == 0 ? np : (MASK & 2) ? n : 0;
+      const uint32_t dflt = g == 1 ? 0xffffffffu : 0u;
+      u32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = k + i < lim ? base[k + i] : dflt;
+      psm = v;
+    }
+    // the stage loads after the small ones (see the dK/dV kernel)
     dma_chunks<St::cKc>(sb, wave, lane, [&](int x) { return kcs + (uint32_t)(x * 16); });
     dma_chunks<St::cRow>(sb + St::offT, wave, lane, [&](int x) { return tks + (uint32_t)(x * 16); });
     dma_chunks<St::cRow>(sb + St::offV, wave, lane, [&](int x) { return rvs + (uint32_t)(x * 16); });
-    if (tid < 16) {
-      psm = reinterpret_cast<const u32x4*>(p.ks + (int64_t)bh * np + key0)[tid];
-    } else if ((MASK & 2) && tid < 32) {
-      const int64_t k = key0 + 4 * (tid - 16);
-      const int32_t* db = p.doc + (int64_t)bidx * n;
-      psm = u32x4{(uint32_t)(k + 0 < n ? db[k + 0] : -1), (uint32_t)(k + 1 < n ? db[k + 1] : -1),
-                  (uint32_t)(k + 2 < n ? db[k + 2] : -1), (uint32_t)(k + 3 < n ? db[k + 3] : -1)};
-    }
   };
   auto store_small = [&](int stage) __attribute__((always_inline)) {
     uint8_t* sb = smem + stage * St::bytes;
@@ -565,36 +573,43 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
     const uint8_t* tds = reinterpret_cast<const uint8_t*>(p.tdo + ((int64_t)bh * np + m0) * D);
     const uint8_t* tqs = reinterpret_cast<const uint8_t*>(p.tq + ((int64_t)bh * np + m0) * D);
     const uint8_t* rds = reinterpret_cast<const uint8_t*>(p.rdo + ((int64_t)bh * np + m0) * D);
+    if (tid < 64) {
+      // one path for the 64 lanes of wave 0 (no per-lane branches writing the
+      // same registers, which would make the compiler wait for loads in
+      // flight, the stage loads included): lanes 16g .. 16g+15 take values
+      // 4(lane&15) .. +3 of the Q scales (g=0), LSE (g=1, -inf past N), D
+      // (g=2) or query document ids (g=3, -1 past N)
+      const int g = tid >> 4;
+      const int64_t m = m0 + 4 * (tid & 15);
+      const uint32_t* base = g == 0   ? reinterpret_cast<const uint32_t*>(p.qs + (int64_t)bh * np)
+                             : g == 1 ? reinterpret_cast<const uint32_t*>(p.lse + (int64_t)bh * n)
+                             : g == 2 ? reinterpret_cast<const uint32_t*>(p.delta + (int64_t)bh * np)
+                             : (MASK & 2) ? reinterpret_cast<const uint32_t*>(p.doc + (int64_t)bidx * n)
+                                          : reinterpret_cast<const uint32_t*>(p.qs);  // not read
+      const int64_t lim = (g == 0 || g == 2) ? np : (g == 1 || (MASK & 2)) ? n : 0;
+      const uint32_t dflt = g == 1 ? __float_as_uint(-INFINITY) : g == 3 ? 0xffffffffu : 0u;
+      u32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = m + i < lim ? base[m + i] : dflt;
+      psm = v;
+    }
+    // the stage loads after the small ones: a wait for the small values then
+    // leaves the stage loads in flight
     dma_chunks<St::cQc>(sb, wave, lane, [&](int x) { return qcs + (uint32_t)(x * 16); });
     dma_chunks<St::cRow>(sb + St::offTdo, wave, lane, [&](int x) { return tds + (uint32_t)(x * 16); });
     dma_chunks<St::cRow>(sb + St::offTq, wave, lane, [&](int x) { return tqs + (uint32_t)(x * 16); });
     dma_chunks<St::cRow>(sb + St::offDo, wave, lane, [&](int x) { return rds + (uint32_t)(x * 16); });
-    if (tid < 16) {
-      psm = reinterpret_cast<const u32x4*>(p.qs + (int64_t)bh * np + m0)[tid];
-    } else if (tid < 32) {
-      // the LSE, +inf for rows with no gradient (past N, or no visible key in
-      // the forward): 2^(s - inf) = 0 needs no per-element test
-      const int64_t m = m0 + 4 * (tid - 16);
-      const float* lb = p.lse + (int64_t)bh * n;
-      float l4[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float l = m + i < n ? lb[m + i] : -INFINITY;
-        l4[i] = l > -INFINITY ? l : INFINITY;
-      }
-      psm = u32x4{__float_as_uint(l4[0]), __float_as_uint(l4[1]), __float_as_uint(l4[2]), __float_as_uint(l4[3])};
-    } else if (tid < 48) {
-      psm = reinterpret_cast<const u32x4*>(p.delta + (int64_t)bh * np + m0)[tid - 32];
-    } else if ((MASK & 2) && tid < 64) {
-      const int64_t m = m0 + 4 * (tid - 48);
-      const int32_t* db = p.doc + (int64_t)bidx * n;
-      psm = u32x4{(uint32_t)(m + 0 < n ? db[m + 0] : -1), (uint32_t)(m + 1 < n ? db[m + 1] : -1),
-                  (uint32_t)(m + 2 < n ? db[m + 2] : -1), (uint32_t)(m + 3 < n ? db[m + 3] : -1)};
-    }
   };
   auto store_small = [&](int stage) __attribute__((always_inline)) {
     uint8_t* sb = smem + stage * St::bytes;
-    if (tid < 48 || ((MASK & 2) && tid < 64)) reinterpret_cast<u32x4*>(sb + St::offQd)[tid] = psm;
+    u32x4 v = psm;
+    if (tid >= 16 && tid < 32) {
+      // +inf for rows with no gradient (past N, or no visible key in the
+      // forward): 2^(s - inf) = 0 needs no per-element test
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(v[i]) > -INFINITY ? v[i] : __float_as_uint(INFINITY);
+    }
+    if (tid < 48 || ((MASK & 2) && tid < 64)) reinterpret_cast<u32x4*>(sb + St::offQd)[tid] = v;
   };
 
   int s = next_active(0);
