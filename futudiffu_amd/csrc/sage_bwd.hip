@@ -378,6 +378,14 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
       const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
       const int4* dkl = reinterpret_cast<const int4*>(sb + St::offDoc);
       const int kmax = (int)min((int64_t)64, n - (int64_t)t * 64);  // valid keys of this tile
+      // the K~ operands of dQ += dS . K~, read before the P / dS vector work
+      // so their LDS latency hides under it
+      const bf16x8* tkl = reinterpret_cast<const bf16x8*>(sb + St::offT);
+      bf16x8 tkf[NC][2];
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) tkf[c][tt] = tkl[((c * 2 + b) * 2 + tt) * 64 + lane];
       bf16x8 dsa[2];
       // s - lse = acc * (qd * kd) - lse; keys past N (the last tile only) are
       // hidden by a test taken on that tile alone
@@ -403,13 +411,11 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
       else
         scores(std::false_type{});
       // dQ += dS . K~ over this key half
-      const bf16x8* tkl = reinterpret_cast<const bf16x8*>(sb + St::offT);
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
-          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(dsa[tt], tkl[((c * 2 + b) * 2 + tt) * 64 + lane], acc[c],
-                                                           0, 0, 0);
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(dsa[tt], tkf[c][tt], acc[c], 0, 0, 0);
     }
     if (tn < nt) store_small(stage ^ 1);
     wait_vmem();
