@@ -845,6 +845,17 @@ __global__ void __launch_bounds__(256) merge_split_kernel(AttnParams p) {
   const float* slots = p.part + si * parts * kPartFloats<D>;
   __shared__ float fac[kMaxParts][8];  // rows 8j .. 8j + 7 of the block
   const int tid = threadIdx.x;
+  // the partial O values first: they do not depend on the factors, so both
+  // rounds of loads are in flight together
+  const int c = tid >> 6, lane = tid & 63, h = lane >> 5, r = lane & 31;
+  float x[kMaxParts][4];
+  if (tid < NC * 64) {
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        x[q][i] = q < parts ? slots[q * kPartFloats<D> + ((w * NC + c) * 16 + 4 * j + i) * 64 + lane] : 0.0f;
+  }
   if (tid < 8) {
     const int row = 8 * j + tid;
     float m[kMaxParts], l[kMaxParts];
@@ -875,13 +886,6 @@ __global__ void __launch_bounds__(256) merge_split_kernel(AttnParams p) {
   }
   __syncthreads();
   if (tid < NC * 64) {
-    const int c = tid >> 6, lane = tid & 63, h = lane >> 5, r = lane & 31;
-    float x[kMaxParts][4];
-#pragma unroll
-    for (int q = 0; q < kMaxParts; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        x[q][i] = q < parts ? slots[q * kPartFloats<D> + ((w * NC + c) * 16 + 4 * j + i) * 64 + lane] : 0.0f;
     const int bh_b = bh / p.h, bh_h = bh - bh_b * p.h;
     uint16_t* ob = p.out + bh_b * p.out_bs + bh_h * p.out_hs + q0 * p.out_rs + 32 * c + r;
 #pragma unroll
