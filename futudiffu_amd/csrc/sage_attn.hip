@@ -434,14 +434,20 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
       pa[b][e >> 3][e & 7] = (__bf16)pr;
     }
   l_acc += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+  // V fragments read four MFMAs ahead of their use: the chain waits for one
+  // LDS latency, not one per MFMA
   const bf16x8* vl = reinterpret_cast<const bf16x8*>(sb + St::offV);
+  constexpr int kPV = NC * 4, kAhead = 4;
+  bf16x8 vf[kPV];
 #pragma unroll
-  for (int c = 0; c < NC; ++c)
+  for (int i = 0; i < kAhead; ++i) vf[i] = vl[i * 64 + lane];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-        o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[b][tt], vl[((c * 2 + b) * 2 + tt) * 64 + lane], o[c], 0, 0, 0);
+  for (int i = 0; i < kPV; ++i) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int c = i >> 2, b = (i >> 1) & 1, tt = i & 1;  // fragment ((c * 2 + b) * 2 + tt) = i
+    o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[b][tt], vf[i], o[c], 0, 0, 0);
+    if (i + kAhead < kPV) vf[i + kAhead] = vl[(i + kAhead) * 64 + lane];
+  }
 }
 
 // Tiles [t_begin, t_end) of work item (bh, query tile qt) for this wave:
