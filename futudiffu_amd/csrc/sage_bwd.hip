@@ -673,15 +673,25 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
           db[e >> 3][e & 7] = (__bf16)(ds * p.sm_scale);
         }
       }
-      // dV^T += dO^T . P, dK^T += Q^T . dS over this query half
+      // dV^T += dO^T . P, dK^T += Q^T . dS over this query half; operand
+      // fragments read two MFMA pairs ahead of their use
+      constexpr int kPairs = NC * 2, kAhead = 2;
+      bf16x8 tdf[kPairs], tqf[kPairs];
+      auto frag = [&](int i) __attribute__((always_inline)) {
+        const int ci = (((i >> 1) * 2 + a) * 2 + (i & 1)) * 64 + lane;  // c = i / 2, tt = i % 2
+        tdf[i] = tdl[ci];
+        tqf[i] = tql[ci];
+      };
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+      for (int i = 0; i < kAhead; ++i) frag(i);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int ci = ((c * 2 + a) * 2 + tt) * 64 + lane;
-          dva[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tdl[ci], pb[tt], dva[c], 0, 0, 0);
-          dka[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tql[ci], db[tt], dka[c], 0, 0, 0);
-        }
+      for (int i = 0; i < kPairs; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int c = i >> 1, tt = i & 1;
+        dva[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tdf[i], pb[tt], dva[c], 0, 0, 0);
+        dka[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tqf[i], db[tt], dka[c], 0, 0, 0);
+        if (i + kAhead < kPairs) frag(i + kAhead);
+      }
     }
     if (sn < nsteps) store_small(stage ^ 1);
     wait_vmem();
