@@ -369,10 +369,14 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
       // dP^T = V . dO^T
       f32x16 dp = f32x16{0};
       const u32x4* vl = reinterpret_cast<const u32x4*>(sb + St::offV);
+      u32x4 vf[2 * NC];  // V[key 32b + r][16c2 + 8h, +8), read two MFMAs ahead
+      vf[0] = vl[(b * 2 * NC + 0) * 64 + lane];
+      vf[1] = vl[(b * 2 * NC + 1) * 64 + lane];
 #pragma unroll
       for (int c2 = 0; c2 < 2 * NC; ++c2) {
-        const u32x4 w = vl[(b * 2 * NC + c2) * 64 + lane];  // V[key 32b + r][16c2 + 8h, +8)
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), dof[c2], dp, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vf[c2]), dof[c2], dp, 0, 0, 0);
+        if (c2 + 2 < 2 * NC) vf[c2 + 2] = vl[(b * 2 * NC + c2 + 2) * 64 + lane];
       }
       // P^T, dS^T (bf16, packed as the A operand of dS . K~)
       const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
@@ -643,14 +647,21 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) qa[c] = reinterpret_cast<const i32x4*>(sb)[(a * NC + c) * 64 + lane];
       const SAcc sacc = score_block<D, QK>(qa, kf);
-      // dP = dO . V^T
+      // dP = dO . V^T, operands read two MFMAs ahead of their use
       f32x16 dp = f32x16{0};
+      u32x4 wf[2 * NC], vf[2 * NC];
+      auto dpfrag = [&](int c2) __attribute__((always_inline)) {
+        wf[c2] = dol[(a * 2 * NC + c2) * 64 + lane];   // dO[query 32a + r][16c2 + 8h, +8)
+        vf[c2] = vrl[(kg * 2 * NC + c2) * 64 + lane];  // V[krow][16c2 + 8h, +8)
+      };
+      dpfrag(0);
+      dpfrag(1);
 #pragma unroll
       for (int c2 = 0; c2 < 2 * NC; ++c2) {
-        const u32x4 w = dol[(a * 2 * NC + c2) * 64 + lane];    // dO[query 32a + r][16c2 + 8h, +8)
-        const u32x4 vv = vrl[(kg * 2 * NC + c2) * 64 + lane];  // V[krow][16c2 + 8h, +8)
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, vv),
-                                                     dp, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[c2]),
+                                                     __builtin_bit_cast(bf16x8, vf[c2]), dp, 0, 0, 0);
+        if (c2 + 2 < 2 * NC) dpfrag(c2 + 2);
       }
       bf16x8 pb[2], db[2];
 #pragma unroll
