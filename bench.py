@@ -74,6 +74,8 @@ CASES = {
     "dit512_b1h30n1280": dict(B=1, H=30, N=1280, D=128, qk="int8", pv="fp8", gran="token"),
     "dit1280x832_int8fp8": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="fp8", gran="token"),
     "dit1280x832_fp8bf16": dict(B=1, H=30, N=4416, D=128, qk="fp8", pv="bf16", gran="token"),
+    # the reference's fp8 LSE variant (fp8 QK, fp8 P.V: sage_attention.py:316-323)
+    "dit1280x832_fp8fp8": dict(B=1, H=30, N=4416, D=128, qk="fp8", pv="fp8", gran="token"),
     # the production variant of futudiffu_ii::sage_attn_masked (int8 QK, bf16
     # P.V), unmasked and with the packed batch's reference tile mask
     "dit1280x832_int8bf16": dict(B=1, H=30, N=4416, D=128, qk="int8", pv="bf16", gran="token"),

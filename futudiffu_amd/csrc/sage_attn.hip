@@ -576,9 +576,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
   }
 
   constexpr int kSt = SM::kStages;
-  // (Taken where its registers fit without spilling: the other fp8 P.V
-  // variants run the general loop below.)
-  constexpr bool kFast = PV == kPV_FP8 && (MASK & 2) == 0 && ((QK == kQK_INT8 && GRAN == kGRAN_TOKEN) || D == 64);
+  constexpr bool kFast = PV == kPV_FP8 && (MASK & 2) == 0;
   if constexpr (kFast) {
     // ---- fp8 P.V, no per-token visibility: every scheduled tile is computed by
     // every live wave, so the product of tile i-1 is always pending in
@@ -649,11 +647,8 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       publish();
       advance();
     }
-    if (t < t_end) {  // last tile: possibly ragged, no successor
-      const uint8_t* sb = sp(stage);
+    if (t < t_end) {  // last tile: the pending product, then the tile with its P.V formed at once
       const uint8_t* sbp = sp(stage_p);
-      const float kdb = kd_block(t);
-      const int kvalid = keys_valid(t);
 #pragma unroll
       for (int c2 = 0; c2 < NC; c2 += 2) {
         f32x16 p0, p1;
@@ -662,15 +657,12 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
         pv_accum(o, c2, p0, p1, rv);
         __builtin_amdgcn_sched_barrier(0);  // one pair's products in flight at a time
       }
-      half_scores<D, QK, PV, GRAN, false>(sb, s0, 0, h, kdb, kvalid, false, dq, u[0]);
-      half_scores<D, QK, PV, GRAN, false>(sb, s1, 1, h, kdb, kvalid, false, dq, u[1]);
-      __builtin_amdgcn_sched_barrier(0);
-      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
-      stage_p = stage;
+      const uint8_t* sb = sp(stage);
+      tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kd_block(t),
+                                              keys_valid(t));
       publish();
       advance();
-    }
-    if (any) {  // the last tile's P.V
+    } else if (any) {  // the single tile was also the first: its product is pending
       const uint8_t* sbp = sp(stage_p);
 #pragma unroll
       for (int c2 = 0; c2 < NC; c2 += 2) {
@@ -678,7 +670,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
         f32x32 rv;
         pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
         pv_accum(o, c2, p0, p1, rv);
-        __builtin_amdgcn_sched_barrier(0);  // one pair's products in flight at a time
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     __syncthreads();  // the ring is reused after
