@@ -48,9 +48,13 @@ constexpr int64_t kPartFloats = 128 * D + 2 * 256;
 
 // Tail split of an unmasked launch of n_items 128-row items of nt key tiles:
 // whole items fill complete rounds of the resident workgroups; the items of
-// the last, partial round are cut into `parts` ranges of key tiles, chosen to
-// minimize (rounds the pieces take) x (tiles per piece + 2 tiles of pipeline
-// start).  Launches of less than one round are not cut: there every item
+// the last, partial round are cut into `parts` ranges of key tiles (at most
+// 4), chosen to minimize (rounds the pieces take) x (tiles per piece + 2
+// tiles of pipeline start).  The cap of 4 is measured: at 1050 items of 69
+// tiles, 4 pieces beat 8 (257.6 vs 260.0 us) and 2 (271.7 us), since the
+// partials' traffic and merge grow with the piece count and the pieces run
+// beside the second round's last items.  Launches of less than one round are
+// not cut: there every item
 // would be cut, and the partials' traffic and the merge then cost more than
 // the balance gains (measured at 300 items of 20 tiles: 50.6 us uncut,
 // 57.9 / 59.8 / 61.9 us in 2 / 3 / 4 pieces).
@@ -64,7 +68,7 @@ inline TailSplit tail_split(int64_t n_items, int64_t nt) {
   const int64_t rest = n_items >= kResidentWGs ? n_items % kResidentWGs : 0;
   if (rest == 0) return t;
   int64_t best = (rest + kResidentWGs - 1) / kResidentWGs * (nt + 2);
-  const int pmax = (int)(nt < 8 ? nt : 8);
+  const int pmax = (int)(nt < 4 ? nt : 4);
   for (int p = 2; p <= pmax; ++p) {
     const int64_t cost = (rest * p + kResidentWGs - 1) / kResidentWGs * ((nt + p - 1) / p + 2);
     if (cost < best) {

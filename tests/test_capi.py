@@ -49,10 +49,11 @@ def test_sizes_and_padding():
     assert lib.sage_quant_workspace_bytes(1, 257, 64) == 2 * 64 * 8
     # per-batch summaries of every 64-key tile and 32- and 128-row query block,
     # then (256-byte aligned) fp32 slots of 128 x D + 512 floats for the pieces
-    # of the split tail: 26 items x 8 pieces at the 1x30x4416x128 headline shape
-    # (1050 items = 2 rounds of 512 + 26), none below one round of 512 items
-    for b, h, n, d, pieces in ((2, 3, 200, 128, 0), (1, 30, 4416, 128, 208), (1, 1, 1, 64, 0),
-                               (1, 30, 1280, 128, 0), (2, 30, 4416, 128, 52 * 8)):
+    # of the split tail: 26 items x 4 pieces (the cap) at the 1x30x4416x128
+    # headline shape (1050 items = 2 rounds of 512 + 26), none below one round
+    # of 512 items
+    for b, h, n, d, pieces in ((2, 3, 200, 128, 0), (1, 30, 4416, 128, 26 * 4), (1, 1, 1, 64, 0),
+                               (1, 30, 1280, 128, 0), (2, 30, 4416, 128, 52 * 4)):
         np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
         doc = (b * (nt + np_ // 32 + np_ // 128) * 16 + 255) // 256 * 256
         assert lib.sage_attn_workspace_bytes(b, h, n, d) == doc + pieces * (128 * d + 512) * 4
