@@ -42,9 +42,12 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    # ~50 ms of work: the GPU clock is still ramping during the first ~20 ms
-    # (attention 318 us per call after 10 warm-up steps, 287 us after 150)
     ap.add_argument("--warmup", type=int, default=150)
+    # The GPU clock ramps during the first tens of milliseconds of work
+    # (attention 318 us per call after 10 warm-up steps, 287 us after 150), so
+    # before the counted warm-up the same op runs, untimed, for a fixed wall
+    # time whatever --warmup says.
+    ap.add_argument("--prewarm-seconds", type=float, default=0.3)
     ap.add_argument("--qk", default="int8", choices=["int8", "fp8"])
     ap.add_argument("--pv", default="fp8", choices=["fp8", "bf16"])
     ap.add_argument("--granularity", default="token", choices=["token", "block64"])
@@ -167,10 +170,7 @@ def cpu_baseline(args, flop_per_head):
     for _ in range(reps):
         O.sage_forward(q, k, v, None, args.qk, args.pv, args.granularity, True)
     per_head = (time.perf_counter() - t0) / reps
-    t0 = time.perf_counter()
-    qf, kf, vf = q.float(), k.float(), v.float()
-    torch.nn.functional.scaled_dot_product_attention(q, k, v)
-    sdpa_head = time.perf_counter() - t0
+    sdpa_head = _median_seconds(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v))
     return {
         "value": round(flop_per_head / per_head / 1e12, 6),
         "unit": "TFLOP/s",
@@ -181,9 +181,36 @@ def cpu_baseline(args, flop_per_head):
                    f"{per_head * 1e3:.1f} ms/head, full call extrapolated x{args.B * args.H}"),
         "ms_per_call_extrapolated": round(per_head * 1e3 * args.B * args.H, 3),
         "sdpa_bf16_cpu_ms_per_head": round(sdpa_head * 1e3, 3),
+        "sdpa_sample": "torch SDPA on the same bf16 head, median of 3 runs after one warm-up run",
         "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
     }
+
+
+def _median_seconds(fn, runs=3):
+    """Median wall time of ``runs`` calls of ``fn`` after one untimed call."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def prewarm(step, seconds):
+    """Run ``step`` untimed until ``seconds`` of wall time have passed (the
+    device synchronized), so the counted warm-up starts at steady clocks."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        for _ in range(4):
+            step()
+        n += 4
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return {"seconds": round(time.perf_counter() - t0, 4), "steps": n}
 
 
 def _cpu_model():
@@ -273,9 +300,8 @@ def _cpu_case(c, q, k, v, block_mask, doc, flop, budget_s):
     if d1 is not None:
         dv = O.doc_visibility(d1.to(torch.int64))
         vis = dv if vis is None else vis & dv
-    t0 = time.perf_counter()
-    torch.nn.functional.scaled_dot_product_attention(q1, k1, v1, attn_mask=None if vis is None else vis[:, None])
-    sdpa = time.perf_counter() - t0
+    am = None if vis is None else vis[:, None]
+    sdpa = _median_seconds(lambda: torch.nn.functional.scaled_dot_product_attention(q1, k1, v1, attn_mask=am))
     return {
         "value": round(flop / heads / per_head / 1e12, 6),
         "unit": "TFLOP/s",
@@ -285,6 +311,7 @@ def _cpu_case(c, q, k, v, block_mask, doc, flop, budget_s):
                    f"of one head (batch 0, head 0) of this case; {per_head * 1e3:.1f} ms/head, "
                    f"throughput on that head's share of the FLOPs"),
         "sdpa_bf16_cpu_ms_per_head": round(sdpa * 1e3, 3),
+        "sdpa_sample": "torch SDPA on the same bf16 head and mask, median of 3 runs after one warm-up run",
         "cpu_model": _cpu_model(),
     }
 
@@ -315,6 +342,7 @@ def backward_case(args, name, c):
         return SA.sage_backward(qd, kd, vd, out, lse, dod, sm, block_mask=bmd, doc_ids=docd, qk=c["qk"],
                                 smooth_k=True)
 
+    prewarm(step, args.prewarm_seconds)
     for _ in range(max(args.warmup // 4, 10)):
         step()
     torch.cuda.synchronize()
@@ -378,6 +406,7 @@ def producer_backward_case(args, name, c):
     def step():
         return SA.qkv_postprocess_backward(*dv, H, D, 1e-5)
 
+    prewarm(step, args.prewarm_seconds)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -461,6 +490,7 @@ def all_configs(args):
                 ev[2].record()
 
         def timed(**kw):
+            prewarm(lambda: step(**kw), args.prewarm_seconds)
             for _ in range(args.warmup):
                 step(**kw)
             torch.cuda.synchronize()
@@ -543,6 +573,7 @@ def main():
             ev[2].record()
         return out
 
+    warm = prewarm(step, args.prewarm_seconds)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -586,6 +617,7 @@ def main():
             "granularity": args.granularity, "parallelism": "single GPU",
         },
         "pct_of_fp8_peak": round(100.0 * flop / (ms_per_step * 1e-3) / 1e12 / PEAK_8BIT_TFLOPS, 2),
+        "prewarm": {**warm, "note": "untimed run of the same op before the counted warm-up (clock ramp)"},
         "roofline": {
             "bound": "mfma",
             "kernel": "attn_fwd_kernel + merge_split_kernel",

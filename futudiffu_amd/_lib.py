@@ -29,7 +29,8 @@ SIGNATURES = {
     "sage_attn_fwd": (_c.c_int, [
         _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_int,
         _P, _I64, _I64, _I64, _P, _P, _c.c_size_t, _P, _c.c_int, _P, _P]),
-    "sage_qk_int32": (_c.c_int, [_P, _P, _I64, _I64, _I64, _P, _P]),
+    "sage_attn_qk_accumulators": (_c.c_int, [
+        _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _P, _c.c_size_t, _P, _P, _P, _P]),
     "sage_build_tile_mask": (_c.c_int, [_P, _I64, _I64, _c.c_int32, _P, _P]),
     "sage_qkv_postprocess": (_c.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_float, _P, _P, _P, _P]),
     "sage_qkv_postprocess_bwd": (_c.c_int, [
@@ -62,7 +63,7 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
-            if lib.sage_abi_version() != 5:
+            if lib.sage_abi_version() != 6:
                 raise RuntimeError("libsage_mi355x.so ABI version mismatch")
             _lib = lib
         return _lib

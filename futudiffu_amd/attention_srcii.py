@@ -196,9 +196,17 @@ def _ext_setup_context(ctx, inputs, output):
     out, lse = output
     ctx.save_for_backward(q, k, v, out, lse, block_mask, doc_ids)
     ctx.args = (sm_scale, qk, smooth_k, rest[0] if rest else "bhnd")
+    ctx.granularity = granularity
 
 
 def _ext_backward(ctx, grad_out, grad_lse):
+    """The backward recomputes P from per-token Q / K codes (as the
+    reference's backward kernels do, sage_kernels.py:1526-1577), which is
+    the forward's P only for granularity "token": a forward with per-64-token
+    scales has an LSE of other scores, so its gradient is refused."""
+    if ctx.granularity != "token":
+        raise ValueError(f"sage_attn_ext backward supports granularity 'token' only, the forward ran with "
+                         f"{ctx.granularity!r}")
     q, k, v, out, lse, block_mask, doc_ids = ctx.saved_tensors
     sm_scale, qk, smooth_k, layout = ctx.args
     if layout == "bnhd":
@@ -246,7 +254,8 @@ def sage_attn_qkv_masked_op(qkv: Tensor, q_norm_weight: Tensor, k_norm_weight: T
                             block_mask: Tensor, n_heads: int, head_dim: int, norm_eps: float,
                             sm_scale: float) -> tuple[Tensor, Tensor]:
     out, lse = sage_forward_from_qkv(qkv, q_norm_weight, k_norm_weight, freqs_cis, n_heads, head_dim, norm_eps,
-                                     sm_scale, block_mask=block_mask, qk="int8", pv="bf16", out_layout="bnhd")
+                                     sm_scale, block_mask=block_mask, qk="int8", pv="bf16",
+                                     smooth_k=_sa._SAGE_SMOOTH_K, out_layout="bnhd")
     return out, lse
 
 
@@ -262,6 +271,7 @@ def _qkv_masked_setup(ctx, inputs, output):
     out, lse = output
     ctx.save_for_backward(qkv, q_norm_weight, k_norm_weight, freqs_cis, block_mask, out, lse)
     ctx.args = (n_heads, head_dim, norm_eps, sm_scale)
+    ctx.smooth_k = _sa._SAGE_SMOOTH_K
 
 
 def _qkv_masked_backward(ctx, grad_out, grad_lse):
@@ -273,7 +283,7 @@ def _qkv_masked_backward(ctx, grad_out, grad_lse):
     q, k, v = _sa.qkv_postprocess(qkv, qw, kw, freqs, n_heads, head_dim, norm_eps)
     shape = q.shape
     dq, dk, dv = sage_bwd_ext_op(q, k, v, _to_bhnd(out, shape), lse, _to_bhnd(grad_out, shape), block_mask, None,
-                                 sm_scale, "int8", True)
+                                 sm_scale, "int8", ctx.smooth_k)
     dqkv = _sa.qkv_postprocess_backward(qkv, qw, kw, freqs, dq, dk, dv, n_heads, head_dim, norm_eps)
     return dqkv, None, None, None, None, None, None, None, None
 

@@ -454,7 +454,9 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
 // leaves the wave's O, reference point and row-sum half in o / m_ref / l_acc
 // (O and l in the frame of m_ref; all zero / -inf for a wave past N).
 // Ends with a workgroup barrier, after which the stage ring may be reused.
-template <int D, int QK, int PV, int GRAN, int MASK>
+// DUMP (int8 QK only) also stores every S^T accumulator pair this loop
+// consumes into p.s_dump, at the point where it is consumed.
+template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false>
 __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, int bh, int qt, int t_begin,
                                            int t_end, f32x16* o, float& m_ref, float& l_acc) {
   using St = Stage<D, PV>;
@@ -555,6 +557,21 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
     return GRAN == kGRAN_TOKEN ? 0.0f : load_uniform(p.ks, (int64_t)bh * (p.np / 64) + tt);
   };
   auto keys_valid = [&](int tt) -> int { return p.n - (int64_t)tt * 64 < 64 ? (int)(p.n - (int64_t)tt * 64) : 64; };
+  // the S^T accumulators of tile tt (keys 64 tt + 32 b + 8 j + 4 h + i of
+  // query q0 + r) as the loop consumes them; only live waves call it, so
+  // q0 + r < Np, and every key index is below 64 nt <= Np
+  auto dump = [&](int tt, const SAcc& a0, const SAcc& a1) __attribute__((always_inline)) {
+    if constexpr (DUMP && QK == kQK_INT8) {
+      int32_t* row = p.s_dump + ((int64_t)bh * p.np + q0 + r) * p.np + (int64_t)tt * 64 + 4 * h;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          row[8 * j + i] = a0[4 * j + i];
+          row[32 + 8 * j + i] = a1[4 * j + i];
+        }
+    }
+  };
 
   // ---- prologue: tiles 0 and 1 of the schedule in stages 0 and 1 --------------
   int t = next_active(t_begin);
@@ -615,6 +632,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
     float u[2][16];
     if (t < t_end) {  // first tile: nothing pending
       if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+      dump(t, s0, s1);
       const float kdb = kd_block(t);
       const int kvalid = keys_valid(t);
       half_scores<D, QK, PV, GRAN, false>(sp(stage), s0, 0, h, kdb, kvalid, false, dq, u[0]);
@@ -630,6 +648,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       const uint8_t* sb = sp(stage);
       const uint8_t* sbp = sp(stage_p);
       const float kdb = kd_block(t);
+      dump(t, s0, s1);
       f32x16 p0, p1;
       f32x32 rv;
       pv_issue<D>(sbp, pa_p, rsc_p, lane, 0, p0, p1, rv);
@@ -658,6 +677,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
         __builtin_amdgcn_sched_barrier(0);  // one pair's products in flight at a time
       }
       const uint8_t* sb = sp(stage);
+      dump(t, s0, s1);
       tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kd_block(t),
                                               keys_valid(t));
       publish();
@@ -690,6 +710,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
     if ((MASK & 2) && cls) cls = classify(qsum, load_uniform(p.kv_sum, (int64_t)bidx * p.nt + t));
     // the last tile recomputes its own S^T in place of a next tile's (unused)
     const uint8_t* sb_next = t1 < t_end ? smem + stage1 * St::bytes : sb;
+    if (cls != 0) dump(t, s0, s1);
     if (cls == 2)
       tile_body<D, QK, PV, GRAN, MASK, true>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kdb,
                                              kvalid);
@@ -782,7 +803,7 @@ __device__ __forceinline__ void store_partial(float* slot, const f32x16* o, floa
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_acc), rs, tid * 4, (128 * D + 256) * 4, 0);
 }
 
-template <int D, int QK, int PV, int GRAN, int MASK>
+template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   using SM = Smem<D, PV>;
   constexpr int NC = D / 32;
@@ -807,7 +828,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
       qt = (int)(pos % nq);
       const int t0 = (int)((int64_t)part * p.nt / p.split_parts);
       const int t1 = (int)((int64_t)(part + 1) * p.nt / p.split_parts);
-      item_tiles<D, QK, PV, GRAN, 0>(p, smem, bh, qt, t0, t1, o, m_ref, l_acc);
+      item_tiles<D, QK, PV, GRAN, 0, DUMP>(p, smem, bh, qt, t0, t1, o, m_ref, l_acc);
       store_partial<D>(p.part + c * kPartFloats<D>, o, m_ref, l_acc);
       return;
     }
@@ -819,7 +840,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   } else {
     item_of(blockIdx.x, (int)gridDim.x, p.bh, nq, p.light_last, bh, qt);
   }
-  item_tiles<D, QK, PV, GRAN, MASK>(p, smem, bh, qt, 0, p.nt, o, m_ref, l_acc);
+  item_tiles<D, QK, PV, GRAN, MASK, DUMP>(p, smem, bh, qt, 0, p.nt, o, m_ref, l_acc);
   store_rows_final<D, PV>(p, smem, bh, qt, o, m_ref, l_acc);
 }
 
@@ -898,41 +919,17 @@ __global__ void __launch_bounds__(256) merge_split_kernel(AttnParams p) {
   }
 }
 
-// int32 QK^T of int8 codes through the attention kernel's MFMA fragments.
-// grid (Np/128, BH, Np/64); wave w covers queries [128*x + 32*w, +32), keys of tile z.
-template <int D>
-__global__ void __launch_bounds__(256) qk_int32_kernel(const uint8_t* __restrict__ qc, const uint8_t* __restrict__ kc,
-                                                       int64_t np, int32_t* __restrict__ s_out) {
-  constexpr int NC = D / 32;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, r = lane & 31;
-  const int bh = blockIdx.y, t = blockIdx.z;
-  const int64_t q0 = (int64_t)blockIdx.x * kRowsPerWG + 32 * wave;
-  const uint8_t* qb = qc + (int64_t)bh * np * D + (q0 >> 5) * (32 * D);
-  const i32x4* kl = reinterpret_cast<const i32x4*>(kc + (int64_t)bh * np * D + (int64_t)t * 64 * D);
-  i32x4 qf[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) qf[c] = *reinterpret_cast<const i32x4*>(qb + (c * 64 + lane) * 16);
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    i32x16 acc = i32x16{0};
-#pragma unroll
-    for (int c = 0; c < NC; ++c) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(b * NC + c) * 64 + lane], qf[c], acc, 0, 0, 0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t key = (int64_t)t * 64 + 32 * b + 8 * j + 4 * h + i;
-        s_out[((int64_t)bh * np + q0 + r) * np + key] = acc[4 * j + i];
-      }
-  }
-}
-
 template <int D, int QK, int PV, int GRAN>
 hipError_t launch_attn_g(int mask, const AttnParams& p, hipStream_t st) {
   const int64_t items = (int64_t)p.bh * (p.np / kRowsPerWG);
   const int64_t n_split = mask == 0 ? items - p.n_whole : 0;
   const dim3 grid((unsigned)(mask == 0 ? p.n_whole + n_split * p.split_parts : items));
-  switch (mask) {
+  // the accumulator dump exists for the int8 QK, per-token, unmasked kernels
+  constexpr bool kDumpable = QK == kQK_INT8 && GRAN == kGRAN_TOKEN;
+  if (p.s_dump != nullptr) {
+    if (!kDumpable || mask != 0) return hipErrorInvalidValue;
+    if constexpr (kDumpable) hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 0, true>), grid, dim3(256), 0, st, p);
+  } else switch (mask) {
     case 0: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 0>), grid, dim3(256), 0, st, p); break;
     case 1: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 1>), grid, dim3(256), 0, st, p); break;
     case 2: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 2>), grid, dim3(256), 0, st, p); break;
@@ -974,19 +971,6 @@ hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, 
   if (d == 128) return launch_attn_d<128>(qk, pv, gran, mask, p, st);
   if (d == 64) return launch_attn_d<64>(qk, pv, gran, mask, p, st);
   return hipErrorInvalidValue;
-}
-
-hipError_t launch_qk_int32(const uint8_t* qc, const uint8_t* kc, int64_t bh, int64_t n, int64_t d, int32_t* s,
-                           hipStream_t st) {
-  const int64_t np = padded_len(n);
-  const dim3 grid((unsigned)(np / kRowsPerWG), (unsigned)bh, (unsigned)(np / 64));
-  if (d == 128)
-    hipLaunchKernelGGL(qk_int32_kernel<128>, grid, dim3(256), 0, st, qc, kc, np, s);
-  else if (d == 64)
-    hipLaunchKernelGGL(qk_int32_kernel<64>, grid, dim3(256), 0, st, qc, kc, np, s);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
 }
 
 AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d) {

@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <string.h>
 
+
 #include "../../include/sage_mi355x.h"
 #include "sage_common.h"
 
@@ -212,11 +213,18 @@ int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* 
   return launch_status(e, "sage_quantize_from_qkv");
 }
 
-int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,
+}  // extern "C"
+
+namespace {
+
+// sage_attn_fwd and its variants: validation, workspace layout and launch.
+// s_dump (int8 QK, per-token scales, no mask only) receives the S^T
+// accumulators the kernel's loop consumes.
+int attn_fwd_impl(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,
                   const void* v_in, const float* v_scale, int64_t b, int64_t h, int64_t n, int64_t d, int qk_kind,
                   int pv_kind, int granularity, const uint8_t* tile_mask, int64_t mask_stride_z, int64_t mask_nq,
                   int64_t mask_nkv, const int32_t* doc_ids, void* workspace, size_t workspace_bytes, void* out,
-                  int out_layout, float* lse, hipStream_t stream) {
+                  int out_layout, float* lse, int32_t* s_dump, const char* name, hipStream_t stream) {
   if (b <= 0 || h <= 0) return fail(SAGE_ERR_ARG, "b=%lld and h=%lld must be positive", (long long)b, (long long)h);
   int st = check_common(b * h, n, d, qk_kind, pv_kind, granularity);
   if (st) return st;
@@ -292,8 +300,33 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
   }
   if ((int64_t)p.bh * nq + 8 * sage::kResidentWGs > 0x7fffffff)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(p.bh * nq));
+  p.s_dump = s_dump;
   hipError_t e = sage::launch_attn(qk_kind, pv_kind, granularity, mask, p, d, (int)b, stream);
-  return launch_status(e, "sage_attn_fwd");
+  return launch_status(e, name);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,
+                  const void* v_in, const float* v_scale, int64_t b, int64_t h, int64_t n, int64_t d, int qk_kind,
+                  int pv_kind, int granularity, const uint8_t* tile_mask, int64_t mask_stride_z, int64_t mask_nq,
+                  int64_t mask_nkv, const int32_t* doc_ids, void* workspace, size_t workspace_bytes, void* out,
+                  int out_layout, float* lse, hipStream_t stream) {
+  return attn_fwd_impl(q_codes, q_scale, k_codes, k_scale, v_in, v_scale, b, h, n, d, qk_kind, pv_kind, granularity,
+                       tile_mask, mask_stride_z, mask_nq, mask_nkv, doc_ids, workspace, workspace_bytes, out,
+                       out_layout, lse, nullptr, "sage_attn_fwd", stream);
+}
+
+int sage_attn_qk_accumulators(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,
+                              const void* v_in, const float* v_scale, int64_t b, int64_t h, int64_t n, int64_t d,
+                              int pv_kind, void* workspace, size_t workspace_bytes, void* out, float* lse,
+                              int32_t* s_out, hipStream_t stream) {
+  if (!s_out) return fail(SAGE_ERR_ARG, "null tensor pointer");
+  return attn_fwd_impl(q_codes, q_scale, k_codes, k_scale, v_in, v_scale, b, h, n, d, SAGE_QK_INT8, pv_kind,
+                       SAGE_GRAN_TOKEN, nullptr, 0, 0, 0, nullptr, workspace, workspace_bytes, out, SAGE_OUT_BHND,
+                       lse, s_out, "sage_attn_qk_accumulators", stream);
 }
 
 size_t sage_attn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) {
@@ -415,17 +448,6 @@ int sage_doc_ids_from_cu_seqlens(const int32_t* cu_seqlens, int64_t b, int64_t n
   if (!cu_seqlens || !doc_ids) return fail(SAGE_ERR_ARG, "null tensor pointer");
   return launch_status(sage::launch_doc_from_cu(cu_seqlens, b, n_segments, n, doc_ids, stream),
                        "sage_doc_ids_from_cu_seqlens");
-}
-
-int sage_qk_int32(const void* q_codes, const void* k_codes, int64_t bh, int64_t n, int64_t d, int32_t* s_out,
-                  hipStream_t stream) {
-  int st = check_common(bh, n, d, SAGE_QK_INT8, SAGE_PV_BF16, SAGE_GRAN_TOKEN);
-  if (st) return st;
-  if (!q_codes || !k_codes || !s_out) return fail(SAGE_ERR_ARG, "null tensor pointer");
-  if (!aligned16(q_codes) || !aligned16(k_codes)) return fail(SAGE_ERR_ALIGN, "codes must be 16-byte aligned");
-  hipError_t e = sage::launch_qk_int32(static_cast<const uint8_t*>(q_codes), static_cast<const uint8_t*>(k_codes),
-                                       bh, n, d, s_out, stream);
-  return launch_status(e, "sage_qk_int32");
 }
 
 }  // extern "C"

@@ -36,6 +36,9 @@ struct AttnParams {
   int n_whole;
   int split_parts;
   float* part;  // (items - n_whole) * split_parts slots of kPartFloats<D> floats
+  // parity only (int8 QK, unmasked): int32 [BH, Np, Np] receives the S^T
+  // accumulators of every tile the kernel's own loop consumes (row = query)
+  int32_t* s_dump;
 };
 
 // Resident workgroups of the attention kernel on MI355X: 256 CUs x 2.
@@ -120,8 +123,6 @@ struct AttnWorkspace {
 };
 AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d);
 size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
-hipError_t launch_qk_int32(const uint8_t* qc, const uint8_t* kc, int64_t bh, int64_t n, int64_t d, int32_t* s,
-                           hipStream_t st);
 hipError_t launch_tile_mask(const int32_t* doc, int64_t nb, int64_t n, int32_t pad_fill, uint8_t* mask,
                             hipStream_t st);
 

@@ -11,6 +11,8 @@ argument meaning and error behaviour) on top of the gfx950 HIP library
 * ``sage_attn_forward_masked_with_lse``    -> :461-531
 * ``sage_attn_backward``                   -> :344-458
 * ``sage_attn_backward_masked``            -> :534-648
+* ``sage_attn_op`` (``futudiffu::sage_attn``) and ``sage_attn_masked_op``
+  (``futudiffu::sage_attn_masked``), with autograd -> :664-690, :740-769
 
 Each call runs two kernels on the current stream: ``sage_quantize_qkv``
 (K smoothing + Q/K/V quantization) and ``sage_attn_fwd``.  All outputs and
@@ -444,14 +446,104 @@ def sage_attn_backward_masked(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse:
     return sage_backward(q, k, v, out, lse, dout, sm_scale, block_mask=block_mask, doc_ids=doc_ids, qk="int8")
 
 
-def qk_int32(q_codes: Tensor, k_codes: Tensor, bh: int, n: int, d: int) -> Tensor:
-    """int32 QK^T of int8 fragment codes through the attention kernel's MFMA path.
+def qk_accumulators(qz: SageQuantized, B: int, H: int) -> tuple[Tensor, Tensor, Tensor]:
+    """The attention forward (int8 QK, per-token scales, no mask) on quantized
+    operands, plus the int32 QK^T accumulators its own loop formed.
 
-    Returns ``[bh, Np, Np]`` int32 (row = query, column = key).
+    Returns ``(out, lse, s)`` with ``s`` int32 ``[B*H, Np, Np]`` (row = query,
+    column = key): the result of ``tl.dot(q_int8, k_int8)``
+    (sage_kernels.py:1451) as the kernel's pipelined loop consumed it, tile
+    by tile.  Entries past ``32*ceil(N/32)`` rows or ``64*ceil(N/64)`` keys
+    stay zero.  Codes quantized with per-64-token scales run with those
+    scales repeated per token (the accumulators depend on the codes only).
     """
+    if qz.qk != "int8":
+        raise ValueError("the accumulator dump covers int8 QK")
     lib = _lib.load()
-    np_ = int(lib.sage_padded_len(n))
-    s = torch.empty(bh, np_, np_, dtype=torch.int32, device=q_codes.device)
-    _lib.check(lib.sage_qk_int32(q_codes.data_ptr(), k_codes.data_ptr(), bh, n, d, s.data_ptr(),
-                                 _stream_handle(q_codes.device)))
-    return s
+    BH, N, D = B * H, qz.n, qz.d
+    dev = qz.q_codes.device
+    qs, ks = qz.q_scale, qz.k_scale
+    if qz.granularity == "block64":
+        qs, ks = (t.repeat_interleave(64, dim=1).contiguous() for t in (qs, ks))
+    wsb = int(lib.sage_attn_workspace_bytes(B, H, N, D))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    out = torch.empty(B, H, N, D, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(BH, N, dtype=torch.float32, device=dev)
+    s = torch.zeros(BH, qz.np_, qz.np_, dtype=torch.int32, device=dev)
+    _lib.check(lib.sage_attn_qk_accumulators(
+        qz.q_codes.data_ptr(), qs.data_ptr(), qz.k_codes.data_ptr(), ks.data_ptr(),
+        qz.v_op.data_ptr(), _ptr(qz.v_scale), B, H, N, D, _PV[qz.pv], ws.data_ptr(), wsb, out.data_ptr(),
+        lse.data_ptr(), s.data_ptr(), _stream_handle(dev)))
+    return out, lse, s
+
+
+# ---- legacy ops (sage_attention.py:664-690, :740-769) ----------------------------------
+#
+# The reference registers these two ops in this module, and its legacy router
+# imports them from here: attention.py:101-103 calls sage_attn_op for
+# unmasked attention, :77-79 calls sage_attn_forward_masked for a uint8 block
+# mask.  Same names, schemas, fake implementations (contiguous [B, H, N, D]
+# output, [B*H, N] fp32 LSE) and autograd formulas.  The backward runs with
+# the variant the forward ran with (the reference reads the module
+# configuration again when its backward runs, :374-376, :413).
+
+@torch.library.custom_op("futudiffu::sage_attn", mutates_args=())
+def sage_attn_op(q: Tensor, k: Tensor, v: Tensor, sm_scale: float) -> tuple[Tensor, Tensor]:
+    """SageAttention forward with the configured variant: returns (out, lse)."""
+    return sage_attn_forward_with_lse(q, k, v, sm_scale)
+
+
+@sage_attn_op.register_fake
+def _sage_attn_op_fake(q, k, v, sm_scale):
+    B, H, N, D = q.shape
+    return q.new_empty(B, H, N, D), q.new_empty(B * H, N, dtype=torch.float32)
+
+
+def _legacy_setup_context(ctx, inputs, output):
+    q, k, v, sm_scale = inputs
+    out, lse = output
+    ctx.save_for_backward(q, k, v, out, lse)
+    ctx.sm_scale = sm_scale
+    ctx.qk = _SAGE_QK_QUANT
+    ctx.smooth_k = _SAGE_SMOOTH_K
+
+
+def _legacy_backward(ctx, grad_out, grad_lse):
+    q, k, v, out, lse = ctx.saved_tensors
+    dq, dk, dv = sage_backward(q, k, v, out, lse, grad_out.contiguous(), ctx.sm_scale, qk=ctx.qk,
+                               smooth_k=ctx.smooth_k)
+    return dq, dk, dv, None
+
+
+sage_attn_op.register_autograd(_legacy_backward, setup_context=_legacy_setup_context)
+
+
+@torch.library.custom_op("futudiffu::sage_attn_masked", mutates_args=())
+def sage_attn_masked_op(q: Tensor, k: Tensor, v: Tensor, block_mask: Tensor,
+                        sm_scale: float) -> tuple[Tensor, Tensor]:
+    """Block-masked SageAttention forward (int8 QK, bf16 PV): returns (out, lse)."""
+    return sage_attn_forward_masked_with_lse(q, k, v, block_mask, sm_scale)
+
+
+@sage_attn_masked_op.register_fake
+def _sage_attn_masked_op_fake(q, k, v, block_mask, sm_scale):
+    B, H, N, D = q.shape
+    return q.new_empty(B, H, N, D), q.new_empty(B * H, N, dtype=torch.float32)
+
+
+def _legacy_masked_setup_context(ctx, inputs, output):
+    q, k, v, block_mask, sm_scale = inputs
+    out, lse = output
+    ctx.save_for_backward(q, k, v, out, lse, block_mask)
+    ctx.sm_scale = sm_scale
+    ctx.smooth_k = _SAGE_SMOOTH_K
+
+
+def _legacy_masked_backward(ctx, grad_out, grad_lse):
+    q, k, v, out, lse, block_mask = ctx.saved_tensors
+    dq, dk, dv = sage_backward(q, k, v, out, lse, grad_out.contiguous(), ctx.sm_scale, block_mask=block_mask,
+                               qk="int8", smooth_k=ctx.smooth_k)
+    return dq, dk, dv, None, None
+
+
+sage_attn_masked_op.register_autograd(_legacy_masked_backward, setup_context=_legacy_masked_setup_context)

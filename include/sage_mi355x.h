@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 5
+#define SAGE_ABI_VERSION 6
 
 enum sage_status {
   SAGE_OK = 0,
@@ -182,6 +182,10 @@ size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
  *                 mask_stride_z (0 broadcasts a 2D mask, sage_attention.py:512-519);
  *                 mask_nq x mask_nkv must equal ceil(N/128) x ceil(N/64).
  *                 0 skips the tile pair (sage_kernels.py:1428-1436).
+ *                 Each byte is read as part of its aligned 4-byte word, so
+ *                 the allocation must stay readable up to the next multiple
+ *                 of 4 bytes past the last entry (hipMalloc and the torch
+ *                 caching allocator hand out 256-byte granules).
  *   doc_ids       optional int32 [B, N] per-token document ids for exact
  *                 masking: key n is visible to query m iff doc[n] >= 0 and
  *                 (doc[m] == doc[n] or doc[m] < 0).  Fully masked tiles issue
@@ -274,12 +278,21 @@ int sage_attn_bwd(const void* q, const void* k, const void* v,
                   void* dq, void* dk, void* dv,
                   hipStream_t stream);
 
-/* Debug/parity: int32 QK^T accumulators of int8 codes through the same MFMA
- * fragments as sage_attn_fwd, s_out int32 [BH, Np, Np] (row = query).
- * Replaces the int32 result of tl.dot(q_int8, k_int8) (sage_kernels.py:1451). */
-int sage_qk_int32(const void* q_codes, const void* k_codes,
-                  int64_t bh, int64_t n, int64_t d,
-                  int32_t* s_out, hipStream_t stream);
+/* Parity: sage_attn_fwd with int8 QK, per-token scales, no mask and the
+ * [B, H, N, D] output, which also stores the int32 QK^T accumulators its own
+ * loop consumes, tile by tile, as that loop forms them (the split tail pieces
+ * included): s_out int32 [B*H, Np, Np], row = query, column = key; entries of
+ * rows below 32*ceil(n/32) and keys below 64*ceil(n/64) are written, others
+ * are left as they were.  Exposes the int32 result of tl.dot(q_int8, k_int8)
+ * (sage_kernels.py:1451).  Other arguments as sage_attn_fwd; slower (the
+ * accumulators are stored from inside the loop). */
+int sage_attn_qk_accumulators(const void* q_codes, const float* q_scale,
+                              const void* k_codes, const float* k_scale,
+                              const void* v_in, const float* v_scale,
+                              int64_t b, int64_t h, int64_t n, int64_t d,
+                              int pv_kind, void* workspace, size_t workspace_bytes,
+                              void* out, float* lse, int32_t* s_out,
+                              hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,14 @@ import torch
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "sage_mi355x.h")
 
+# The validation tests below pass small fake device addresses (16, 32, ...).
+# Each base argument set is itself invalid (no workspace, or a null output),
+# so a call whose one override stops being rejected still returns a status
+# instead of launching; and where a GPU is visible they do not run at all,
+# so a check that regresses can never send a kernel to those addresses.
+fake_addresses = pytest.mark.skipif(torch.cuda.device_count() > 0,
+                                    reason="argument-validation calls with fake device addresses run without a GPU")
+
 
 def _declared():
     text = open(HEADER).read()
@@ -36,7 +44,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), f"{name} declared in the header but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes prototype"
-    assert lib.sage_abi_version() == 5
+    assert lib.sage_abi_version() == 6
 
 
 def test_sizes_and_padding():
@@ -61,7 +69,7 @@ def test_sizes_and_padding():
 
 def _quant_call(lib, **over):
     a = dict(q=16, k=32, v=48, bh=2, n=100, d=128, qk=0, pv=1, gran=0, smooth=1, fold=0.18,
-             qc=64, qs=80, kc=96, ks=112, vo=128, vs=144, km=160, ws=176, wsb=1 << 20, stream=None)
+             qc=64, qs=80, kc=96, ks=112, vo=128, vs=144, km=160, ws=None, wsb=0, stream=None)
     a.update(over)
     return lib.sage_quantize_qkv(a["q"], a["k"], a["v"], a["bh"], a["n"], a["d"], a["qk"], a["pv"], a["gran"],
                                  a["smooth"], a["fold"], a["qc"], a["qs"], a["kc"], a["ks"], a["vo"], a["vs"],
@@ -78,10 +86,11 @@ def _quant_call(lib, **over):
     (dict(vs=None), 1, "v_scale"),
     (dict(k=33), 2, "aligned"),
     (dict(km=None), 1, "k_mean"),
-    (dict(wsb=8), 3, "workspace"),
-    (dict(ws=184), 2, "workspace must be 16-byte aligned"),
+    (dict(ws=176, wsb=8), 3, "workspace"),
+    (dict(ws=184, wsb=1 << 20), 2, "workspace must be 16-byte aligned"),
     (dict(bh=70000), 1, "grid"),
 ])
+@fake_addresses
 def test_quantize_rejects_bad_arguments(over, status, msg):
     from futudiffu_amd import _lib
     lib = _lib.load()
@@ -112,6 +121,7 @@ def _attn_call(lib, **over):
     (dict(layout=2), 1, "out_layout must be 0"),
     (dict(layout=-1), 1, "out_layout must be 0"),
 ])
+@fake_addresses
 def test_attn_rejects_bad_arguments(over, status, msg):
     from futudiffu_amd import _lib
     lib = _lib.load()
@@ -135,19 +145,22 @@ def _prod_args(**over):
     (dict(qw=40), 2, "aligned"),
     (dict(eps=-1.0), 1, "norm_eps"),
 ])
+@fake_addresses
 def test_producer_entries_reject_bad_arguments(over, status, msg):
     from futudiffu_amd import _lib
     lib = _lib.load()
-    assert lib.sage_qkv_postprocess(*_prod_args(**over), 80, 96, 112, None) == status
+    # outputs null / workspace missing: rejected after the producer checks
+    assert lib.sage_qkv_postprocess(*_prod_args(**over), 80, 96, None, None) == status
     assert msg in lib.sage_last_error().decode()
     assert lib.sage_quantize_from_qkv(*_prod_args(**over), 0, 1, 0, 1, 0.18, 128, 144, 160, 176, 192, 208, 224,
-                                      240, 1 << 20, None) == status
+                                      None, 0, None) == status
     assert msg in lib.sage_last_error().decode()
     a = _prod_args(**over)
-    assert lib.sage_qkv_postprocess_bwd(*a[:4], 80, 96, 112, *a[4:], 128, None) == status
+    assert lib.sage_qkv_postprocess_bwd(*a[:4], 80, 96, 112, *a[4:], None, None) == status
     assert msg in lib.sage_last_error().decode()
 
 
+@fake_addresses
 def test_producer_backward_checks_gradient_pointers():
     from futudiffu_amd import _lib
     lib = _lib.load()
@@ -172,7 +185,7 @@ def test_producer_backward_python_glue_checks():
 
 def _bwd_call(lib, **over):
     a = dict(q=16, k=32, v=48, out=64, lse=80, do=96, b=1, h=2, n=300, d=128, qk=0, smooth=1, sm=0.088,
-             sml=0.1275, mask=None, sz=0, nq=3, nkv=5, doc=None, ws=256, wsb=1 << 30, dq=112, dk=128, dv=144,
+             sml=0.1275, mask=None, sz=0, nq=3, nkv=5, doc=None, ws=None, wsb=0, dq=112, dk=128, dv=144,
              stream=None)
     a.update(over)
     return lib.sage_attn_bwd(a["q"], a["k"], a["v"], a["out"], a["lse"], a["do"], a["b"], a["h"], a["n"], a["d"],
@@ -194,9 +207,10 @@ def _bwd_call(lib, **over):
     (dict(mask=256, nkv=4), 1, "block_mask must be 3 x 5"),
     (dict(mask=256, sz=9), 1, "mask_stride_z"),
     (dict(ws=None), 3, "workspace"),
-    (dict(wsb=1000), 3, "workspace of"),
-    (dict(ws=264), 2, "workspace must be 16-byte aligned"),
+    (dict(ws=256, wsb=1000), 3, "workspace of"),
+    (dict(ws=264, wsb=1 << 30), 2, "workspace must be 16-byte aligned"),
 ])
+@fake_addresses
 def test_backward_rejects_bad_arguments(over, status, msg):
     from futudiffu_amd import _lib
     lib = _lib.load()
@@ -231,12 +245,13 @@ def test_backward_python_glue_checks():
         SA.sage_backward(q.float(), q, q, q, lse, q)
 
 
+@fake_addresses
 def test_fused_quantize_entry_checks_outputs():
     from futudiffu_amd import _lib
     lib = _lib.load()
     # v_scale missing for fp8 PV; workspace too small for smoothing
     assert lib.sage_quantize_from_qkv(*_prod_args(), 0, 1, 0, 1, 0.18, 128, 144, 160, 176, 192, None, 224,
-                                      240, 1 << 20, None) == 1
+                                      None, 0, None) == 1
     assert "v_scale" in lib.sage_last_error().decode()
     assert lib.sage_quantize_from_qkv(*_prod_args(), 0, 1, 0, 1, 0.18, 128, 144, 160, 176, 192, 208, 224,
                                       240, 8, None) == 3
@@ -305,3 +320,41 @@ def test_doc_id_builders():
     assert d.tolist() == [[0, 0, 0, 1, 1, -1, -1]] * 2
     v = torch.tensor([[True, False, True]])
     assert BM.build_key_padding_doc_ids(v).tolist() == [[0, -1, 0]]
+
+
+def test_legacy_op_schemas_and_fake_shapes():
+    """futudiffu::sage_attn / ::sage_attn_masked (sage_attention.py:664-690,
+    :740-769) and the module-level names the legacy router imports
+    (attention.py:77-79, :101-103)."""
+    from futudiffu_amd import sage_attention as SA
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    ops = torch.ops.futudiffu
+    assert str(ops.sage_attn.default._schema) == (
+        "futudiffu::sage_attn(Tensor q, Tensor k, Tensor v, float sm_scale) -> (Tensor, Tensor)")
+    assert str(ops.sage_attn_masked.default._schema) == (
+        "futudiffu::sage_attn_masked(Tensor q, Tensor k, Tensor v, Tensor block_mask, float sm_scale) "
+        "-> (Tensor, Tensor)")
+    for name in ("sage_attn_op", "sage_attn_masked_op", "sage_attn_forward_masked", "sage_attn_forward"):
+        assert callable(getattr(SA, name))
+    with FakeTensorMode():
+        # a transposed view, as the legacy router passes it (attention.py:69-70)
+        q = torch.empty(2, 40, 3, 128, dtype=torch.bfloat16).transpose(1, 2)
+        m = torch.empty(1, 1, dtype=torch.uint8)
+        for out, lse in (SA.sage_attn_op(q, q, q, 0.1), SA.sage_attn_masked_op(q, q, q, m, 0.1)):
+            assert out.shape == (2, 3, 40, 128) and out.is_contiguous() and out.dtype == torch.bfloat16
+            assert lse.shape == (6, 40) and lse.dtype == torch.float32
+
+
+def test_ext_backward_refuses_block_scales():
+    """The backward recomputes P from per-token codes, so a forward run with
+    per-64-token scales has no consistent gradient: refused before any work."""
+    from futudiffu_amd import attention_srcii as A
+
+    class Ctx:
+        granularity = "block64"
+        saved_tensors = ()
+        args = (0.1, "int8", True, "bhnd")
+
+    with pytest.raises(ValueError, match="granularity 'token' only"):
+        A._ext_backward(Ctx(), None, None)
+

@@ -92,17 +92,45 @@ def test_quantize_bitexact(cuda, B, H, N, D, qk, pv, gran, smooth):
         _assert_bits_equal(vrows[:, :N], v.reshape(BH, N, D).view(torch.int16), "v_bf16_fragments")
 
 
-@pytest.mark.parametrize("N,D", [(256, 64), (1280, 128), (200, 128), (33, 64)])
-def test_qk_int32_bitexact(cuda, N, D):
+@pytest.mark.parametrize("N,D,pv", [(256, 64, "bf16"), (1280, 128, "fp8"), (1280, 128, "bf16"), (200, 128, "fp8"),
+                                     (33, 64, "fp8"), (4416, 128, "fp8")])
+def test_attention_kernel_int32_accumulators_bitexact(cuda, N, D, pv):
+    """The int32 QK^T accumulators the attention kernel's own loop consumes
+    (stored from inside that loop) equal the exact integer products of the
+    oracle's codes (sage_kernels.py:1451), for ragged and whole tiles."""
     SA = _sa()
     B, H = 1, 2
     q, k, v = O.make_inputs(B, H, N, D, seed=7 + N)
-    qz = SA.quantize_qkv(q.to(cuda), k.to(cuda), v.to(cuda), qk="int8", pv="bf16")
-    s = SA.qk_int32(qz.q_codes, qz.k_codes, B * H, N, D)
+    print(f"int32 accumulators N={N} D={D} int8/{pv}", flush=True)
+    qz = SA.quantize_qkv(q.to(cuda), k.to(cuda), v.to(cuda), qk="int8", pv=pv)
+    out, lse, s = SA.qk_accumulators(qz, B, H)
     torch.cuda.synchronize()
-    oz = O.quantize_all(q, k, v, 1.0 / math.sqrt(D), "int8", "bf16", "token", True)
+    oz = O.quantize_all(q, k, v, 1.0 / math.sqrt(D), "int8", pv, "token", True)
     want = O.qk_int32(oz.qc, oz.kc)
-    _assert_bits_equal(s[:, :N, :N], want, "qk_int32")
+    _assert_bits_equal(s[:, :N, :N], want, "kernel int32 accumulators")
+    # and the same launch's attention is the plain forward's, bit for bit
+    out2, lse2 = SA.attn_from_quantized(qz, B, H)
+    torch.cuda.synchronize()
+    _assert_bits_equal(out, out2, "out of the accumulator launch")
+    _assert_bits_equal(lse, lse2, "lse of the accumulator launch")
+
+
+def test_attention_kernel_int32_accumulators_headline_split_tail(cuda):
+    """At 1x30x4416x128 the last 26 query tiles of head 29 run as 4 key-range
+    pieces each (the split tail): the accumulators of heads 0 and 29, stored
+    from inside the kernel's loop, equal the oracle's integer products."""
+    SA = _sa()
+    B, H, N, D = 1, 30, 4416, 128
+    q, k, v = O.make_inputs(B, H, N, D, seed=5)
+    print("int32 accumulators 1x30x4416x128 int8/fp8", flush=True)
+    qz = SA.quantize_qkv(q.to(cuda), k.to(cuda), v.to(cuda), qk="int8", pv="fp8")
+    _, _, s = SA.qk_accumulators(qz, B, H)
+    torch.cuda.synchronize()
+    for hh in (0, 29):
+        sl = slice(hh, hh + 1)
+        oz = O.quantize_all(q[:, sl], k[:, sl], v[:, sl], 1.0 / math.sqrt(D), "int8", "fp8", "token", True)
+        _assert_bits_equal(s[hh:hh + 1, :N, :N], O.qk_int32(oz.qc, oz.kc), f"head {hh} accumulators")
+    del s
 
 
 def _compare(out, lse, q, k, v, qk, pv, gran, block_mask=None, doc_ids=None, smooth=True, tight=True):
