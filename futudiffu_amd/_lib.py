@@ -29,6 +29,9 @@ SIGNATURES = {
     "sage_attn_fwd": (_c.c_int, [
         _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_int,
         _P, _I64, _I64, _I64, _P, _P, _c.c_size_t, _P, _c.c_int, _P, _P]),
+    "sage_attn_fwd_noalloc": (_c.c_int, [
+        _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_int,
+        _P, _I64, _I64, _I64, _P, _P, _c.c_int, _P, _P]),
     "sage_attn_qk_accumulators": (_c.c_int, [
         _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _P, _c.c_size_t, _P, _P, _P, _P]),
     "sage_build_tile_mask": (_c.c_int, [_P, _I64, _I64, _c.c_int32, _P, _P]),

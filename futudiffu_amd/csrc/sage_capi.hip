@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <string.h>
 
+#include <mutex>
 
 #include "../../include/sage_mi355x.h"
 #include "sage_common.h"
@@ -317,6 +318,68 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale, const void* k_codes
   return attn_fwd_impl(q_codes, q_scale, k_codes, k_scale, v_in, v_scale, b, h, n, d, qk_kind, pv_kind, granularity,
                        tile_mask, mask_stride_z, mask_nq, mask_nkv, doc_ids, workspace, workspace_bytes, out,
                        out_layout, lse, nullptr, "sage_attn_fwd", stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Device scratch of sage_attn_fwd_noalloc: the document-id summaries and the
+// split-tail partials that sage_attn_fwd keeps in its workspace argument.
+// Each GPU the library runs on holds its own copy until the process ends.
+// Host code never uses the array's name as an address: its device address
+// comes from hipGetSymbolAddress, once per device, with that device current.
+__device__ __align__(256) uint8_t scratch[SAGE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Scratch address on the device of `stream`, which must be the current device.
+int scratch_of_stream(hipStream_t stream, void** ptr) {
+  int cur = -1, sdev = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess) e = hipStreamGetDevice(stream, &sdev);
+  if (e != hipSuccess) return fail(SAGE_ERR_LAUNCH, "device of the stream: %s", hipGetErrorString(e));
+  if (sdev != cur)
+    return fail(SAGE_ERR_ARG, "the stream belongs to device %d, the current device is %d", sdev, cur);
+  if (cur < 0 || cur >= kMaxDevices) return fail(SAGE_ERR_ARG, "device %d beyond the first %d", cur, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[cur]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(SAGE_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[cur] = p;
+  }
+  *ptr = g_scratch_ptr[cur];
+  return SAGE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sage_attn_fwd_noalloc(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,
+                          const void* v_in, const float* v_scale, int64_t b, int64_t h, int64_t n, int64_t d,
+                          int qk_kind, int pv_kind, int granularity, const uint8_t* tile_mask, int64_t mask_stride_z,
+                          int64_t mask_nq, int64_t mask_nkv, const int32_t* doc_ids, void* out, int out_layout,
+                          float* lse, hipStream_t stream) {
+  if (b <= 0 || h <= 0) return fail(SAGE_ERR_ARG, "b=%lld and h=%lld must be positive", (long long)b, (long long)h);
+  int st = check_common(b * h, n, d, qk_kind, pv_kind, granularity);
+  if (st) return st;
+  const size_t need = sage::attn_workspace_bytes(b, h, n, d);
+  if (need > (size_t)SAGE_NOALLOC_SCRATCH_BYTES)
+    return fail(SAGE_ERR_WORKSPACE,
+                "b=%lld h=%lld n=%lld d=%lld needs %zu bytes of workspace, beyond the %zu-byte scratch of the "
+                "allocation-free entry point; use sage_attn_fwd with a workspace",
+                (long long)b, (long long)h, (long long)n, (long long)d, need, (size_t)SAGE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  st = scratch_of_stream(stream, &ws);
+  if (st) return st;
+  return attn_fwd_impl(q_codes, q_scale, k_codes, k_scale, v_in, v_scale, b, h, n, d, qk_kind, pv_kind, granularity,
+                       tile_mask, mask_stride_z, mask_nq, mask_nkv, doc_ids, ws, SAGE_NOALLOC_SCRATCH_BYTES, out,
+                       out_layout, lse, nullptr, "sage_attn_fwd_noalloc", stream);
 }
 
 int sage_attn_qk_accumulators(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,

@@ -210,6 +210,34 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale,
                   void* out, int out_layout, float* lse,
                   hipStream_t stream);
 
+/* Bytes of device scratch behind sage_attn_fwd_noalloc (per GPU). */
+#define SAGE_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* sage_attn_fwd without the workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace lives in a fixed device array of SAGE_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends; shapes whose sage_attn_workspace_bytes
+ * exceed it are rejected with SAGE_ERR_WORKSPACE before any launch (the
+ * 1x30x4416x128 headline needs 6.9 MB).  The call allocates and frees
+ * nothing and needs no memory cleared beforehand: every byte of scratch it
+ * reads was written earlier in the same call.  Every call on one GPU shares
+ * that GPU's scratch, so calls that overlap on one GPU (other streams, other
+ * threads) race; calls ordered on one stream do not.  The stream must belong
+ * to the current device.  The first call on a device looks the array's
+ * address up (hipGetSymbolAddress).  Other arguments, results and errors as
+ * sage_attn_fwd, bit-identical to it. */
+int sage_attn_fwd_noalloc(const void* q_codes, const float* q_scale,
+                          const void* k_codes, const float* k_scale,
+                          const void* v_in, const float* v_scale,
+                          int64_t b, int64_t h, int64_t n, int64_t d,
+                          int qk_kind, int pv_kind, int granularity,
+                          const uint8_t* tile_mask, int64_t mask_stride_z,
+                          int64_t mask_nq, int64_t mask_nkv,
+                          const int32_t* doc_ids,
+                          void* out, int out_layout, float* lse,
+                          hipStream_t stream);
+
 /* Reference tile mask from device per-token document ids.
  * Replaces the host construction of build_block_mask /
  * build_block_mask_from_packing_info (src_ii/block_mask.py:35-129): Q tile i

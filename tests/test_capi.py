@@ -358,3 +358,23 @@ def test_ext_backward_refuses_block_scales():
     with pytest.raises(ValueError, match="granularity 'token' only"):
         A._ext_backward(Ctx(), None, None)
 
+
+@fake_addresses
+def test_noalloc_entry_rejects_shapes_beyond_its_scratch():
+    """The allocation-free entry point keeps its workspace in a fixed 16 MiB
+    device array: 1x32x4480x128 (96 tail items in 4 pieces, 25 MB of
+    partials) is refused before any device call; argument checks match
+    sage_attn_fwd's."""
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    assert lib.sage_attn_workspace_bytes(1, 32, 4480, 128) > 16 << 20
+    assert lib.sage_attn_workspace_bytes(1, 30, 4416, 128) <= 16 << 20
+    args = [16, 32, 48, 64, 80, 96, 1, 32, 4480, 128, 0, 1, 0, None, 0, 0, 0, None, 112, 0, 128, None]
+    assert lib.sage_attn_fwd_noalloc(*args) == 3
+    assert "beyond the 16777216-byte scratch" in lib.sage_last_error().decode()
+    args[9] = 96
+    assert lib.sage_attn_fwd_noalloc(*args) == 1
+    assert "head_dim" in lib.sage_last_error().decode()
+    args[9], args[6] = 128, 0
+    assert lib.sage_attn_fwd_noalloc(*args) == 1
+    assert "positive" in lib.sage_last_error().decode()
