@@ -525,22 +525,23 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
   // the stage.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   int4 pre_doc = make_int4(-1, -1, -1, -1);
+  // buffer resources over this head's K and V operands and scales: the stage
+  // copies take a scalar tile offset and a loop-invariant lane offset
+  const __amdgpu_buffer_rsrc_t rs_k = raw_rsrc(kg, (uint32_t)(p.np * D));
+  const __amdgpu_buffer_rsrc_t rs_v = raw_rsrc(vg, (uint32_t)(p.np / 64 * St::vBytes));
+  const __amdgpu_buffer_rsrc_t rs_ks = raw_rsrc(p.ks + (int64_t)bh * p.np, (uint32_t)(p.np * 4));
+  const __amdgpu_buffer_rsrc_t rs_vs =
+      raw_rsrc(PV == kPV_FP8 ? p.vs + (int64_t)bh * (p.np / 64) * D : p.ks, (uint32_t)(p.np / 64 * D * 4));
   auto load_tile = [&](int tt, uint8_t* sbw) __attribute__((always_inline)) {
-    const uint8_t* ksrc = kg + (int64_t)tt * 64 * D;
-    const uint8_t* vsrc = vg + (int64_t)tt * St::vBytes;
-    // uniform base + 32-bit lane offset: the scalar-base addressing form
-    dma_chunks<St::cK, 4>(sbw, wave_u, lane, [&](int x) { return ksrc + (uint32_t)(x * 16); });
-    dma_chunks<St::cV, 4>(sbw + St::offV, wave_u, lane, [&](int x) { return vsrc + (uint32_t)(x * 16); });
+    dma_chunks_buf<St::cK, 4>(sbw, wave_u, lane, rs_k, tt * 64 * D);
+    dma_chunks_buf<St::cV, 4>(sbw + St::offV, wave_u, lane, rs_v, tt * St::vBytes);
     if (wave_u == 0) {
-      const bool kd_lane = GRAN == kGRAN_TOKEN && lane < 16;
-      const bool vd_lane = PV == kPV_FP8 && lane >= 16 && lane < 16 + D / 4;
-      if (kd_lane || vd_lane) {
-        const uint8_t* src =
-            kd_lane ? reinterpret_cast<const uint8_t*>(p.ks + (int64_t)bh * p.np + (int64_t)tt * 64) + (uint32_t)(lane * 16)
-                    : reinterpret_cast<const uint8_t*>(p.vs + ((int64_t)bh * (p.np / 64) + tt) * D) +
-                          (uint32_t)((lane - 16) * 16);
-        __builtin_amdgcn_global_load_lds(src, sbw + St::offKd, 16, 0, 0);
-      }
+      // K scales by lanes 0..15 (64 keys), V scales by lanes 16.. (D
+      // channels); lane l lands at byte 16 l of the scale region
+      if (GRAN == kGRAN_TOKEN && lane < 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ks, sbw + St::offKd, 16, lane * 16, tt * 256, 0, 0);
+      if (PV == kPV_FP8 && lane >= 16 && lane < 16 + D / 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_vs, sbw + St::offKd, 16, (lane - 16) * 16, tt * D * 4, 0, 0);
     }
     if ((MASK & 2) && tid >= 48 && tid < 64) {
       const int64_t base = (int64_t)tt * 64 + (tid - 48) * 4;

@@ -25,6 +25,8 @@ int fail(int code, const char* fmt, ...) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+constexpr int64_t kAttnMaxN = (int64_t)1 << 22;  // sage_attn_fwd's sequence-length limit
+
 int check_common(int64_t bh, int64_t n, int64_t d, int qk, int pv, int gran) {
   if (bh <= 0 || n <= 0) return fail(SAGE_ERR_ARG, "bh=%lld and n=%lld must be positive", (long long)bh, (long long)n);
   if (d != 64 && d != 128) return fail(SAGE_ERR_ARG, "head_dim must be 64 or 128, got %lld", (long long)d);
@@ -238,6 +240,9 @@ int attn_fwd_impl(const void* q_codes, const float* q_scale, const void* k_codes
   if (v_scale && !aligned16(v_scale)) return fail(SAGE_ERR_ALIGN, "v_scale must be 16-byte aligned");
   if (out_layout != SAGE_OUT_BHND && out_layout != SAGE_OUT_BNHD)
     return fail(SAGE_ERR_ARG, "out_layout must be 0 ([B,H,N,D]) or 1 ([B,N,H,D]), got %d", out_layout);
+  // one head's operands are addressed through buffer resources with 32-bit
+  // byte offsets: Np*D*2 bytes of bf16 V must stay below 2^31
+  if (n > kAttnMaxN) return fail(SAGE_ERR_ARG, "n=%lld exceeds %lld for the attention", (long long)n, (long long)kAttnMaxN);
   // The epilogue addresses 32 output rows of one head in 32-bit byte offsets:
   // at most 32 * h*d*2 bytes, under 2^31 since b*h <= 65535 and d <= 128.
   const int64_t nq = (n + 127) / 128, nkv = (n + 63) / 64;

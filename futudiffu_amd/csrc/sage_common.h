@@ -43,7 +43,10 @@ __device__ __forceinline__ uint32_t pack_fp8x2(float a, float b) {
 }
 
 __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float d) {
-  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  // the "old" operand only supplies the high half, which the second convert
+  // overwrites: passing a's bits lets the result share a's register instead
+  // of a zeroed one
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 
@@ -92,6 +95,24 @@ __device__ __forceinline__ void dma_chunks(uint8_t* lds, int wave, int lane, Src
   }
 }
 
+// dma_chunks through a buffer resource: chunk x of the region that starts
+// at byte `soff` of resource `rs` lands at LDS chunk x (the same split over
+// waves).  The lane part of the offset is loop-invariant; the region and
+// block parts are scalar, so no vector register holds an address.  Loads
+// past the resource's size return zeros.
+template <int C, int WAVES>
+__device__ __forceinline__ void dma_chunks_buf(uint8_t* lds, int wave, int lane, __amdgpu_buffer_rsrc_t rs,
+                                               int soff) {
+  static_assert(C % 64 == 0, "whole 64-chunk blocks");
+#pragma unroll
+  for (int j0 = 0; j0 < C / 64; j0 += WAVES) {
+    const int j = j0 + wave;
+    if (C / 64 % WAVES == 0 || j < C / 64)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds + j * 1024, 16, (wave * 64 + lane) * 16, soff + j0 * 1024,
+                                               0, 0);
+  }
+}
+
 // Loads at a workgroup-uniform index through the constant address space, so
 // the compiler emits scalar loads: they wait on the scalar counter, not behind
 // direct global -> LDS loads in flight (which a vector load's vmcnt wait would
@@ -111,6 +132,11 @@ __device__ __forceinline__ uint32_t load_uniform_u8(const uint8_t* base, int64_t
   const uintptr_t a = reinterpret_cast<uintptr_t>(base + i);
   const uint32_t w = *(ConstPtr)(a & ~(uintptr_t)3);
   return (w >> (8 * (a & 3))) & 0xffu;
+}
+
+// Raw (untyped) buffer resource over `bytes` bytes at `base`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left free; gfx9 encoding).

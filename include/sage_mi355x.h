@@ -190,6 +190,8 @@ size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
  *                 masking: key n is visible to query m iff doc[n] >= 0 and
  *                 (doc[m] == doc[n] or doc[m] < 0).  Fully masked tiles issue
  *                 no MFMA.
+ *   n             at most 2^22 (one head's operands are addressed with
+ *                 32-bit byte offsets).
  *   h             heads per batch (row z of q belongs to batch z / h).
  *   workspace     device memory of sage_attn_workspace_bytes(b, h, n, d)
  *                 bytes, 16-byte aligned.  Concurrent calls need separate

@@ -120,6 +120,7 @@ def _attn_call(lib, **over):
     (dict(pv=1, vs=None), 1, "v_scale"),
     (dict(layout=2), 1, "out_layout must be 0"),
     (dict(layout=-1), 1, "out_layout must be 0"),
+    (dict(n=(1 << 22) + 1, nq=0, nkv=0), 1, "exceeds 4194304"),
 ])
 @fake_addresses
 def test_attn_rejects_bad_arguments(over, status, msg):
