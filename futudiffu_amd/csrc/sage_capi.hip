@@ -26,6 +26,9 @@ int fail(int code, const char* fmt, ...) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 constexpr int64_t kAttnMaxN = (int64_t)1 << 22;  // sage_attn_fwd's sequence-length limit
+// Workgroups of one 1D launch of 256-thread workgroups (the dispatch packet
+// holds the grid in work-items, a 32-bit count).
+constexpr int64_t kMaxGridUnits = ((int64_t)1 << 24) - 1;
 
 int check_common(int64_t bh, int64_t n, int64_t d, int qk, int pv, int gran) {
   if (bh <= 0 || n <= 0) return fail(SAGE_ERR_ARG, "bh=%lld and n=%lld must be positive", (long long)bh, (long long)n);
@@ -74,6 +77,9 @@ int check_quant_outputs(int64_t bh, int64_t n, int64_t d, int pv_kind, int smoot
   for (const void* p : ptrs)
     if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
   if (v_scale && !aligned16(v_scale)) return fail(SAGE_ERR_ALIGN, "v_scale must be 16-byte aligned");
+  if (sage::quant_grid_units(bh, n, d) > kMaxGridUnits)
+    return fail(SAGE_ERR_ARG, "quantizing bh=%lld x n=%lld takes %lld workgroups, beyond one launch's %lld",
+                (long long)bh, (long long)n, (long long)sage::quant_grid_units(bh, n, d), (long long)kMaxGridUnits);
   if (smooth_k) {
     if (!k_mean) return fail(SAGE_ERR_ARG, "smooth_k needs k_mean");
     const size_t need = sage::quant_workspace_bytes(bh, n, d);
@@ -98,8 +104,11 @@ int check_producer(const void* qkv, const float* q_norm_w, const float* k_norm_w
     if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
   if (!(norm_eps >= 0.0f)) return fail(SAGE_ERR_ARG, "norm_eps must be >= 0");
   // one workgroup per (64-token block, head) in a 1D grid
-  if (b * h * ((n + 63) / 64) > 0x7fffffff)
+  if (b * h * ((n + 63) / 64) > kMaxGridUnits)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/64) = %lld exceeds the grid limit", (long long)(b * h * ((n + 63) / 64)));
+  // 256 token rows of the projection output (3*h*d bf16 each) within 32-bit byte offsets
+  if (3 * h * d * 2 * 256 > (int64_t)0xffffffff)
+    return fail(SAGE_ERR_ARG, "3*h*d = %lld channels per token row is too wide for the producer", (long long)(3 * h * d));
   prod = sage::ProdArgs{static_cast<const uint16_t*>(qkv), q_norm_w, k_norm_w, freqs, (int)h, (int)(b * h),
                         norm_eps};
   return SAGE_OK;
@@ -304,7 +313,7 @@ int attn_fwd_impl(const void* q_codes, const float* q_scale, const void* k_codes
     p.split_parts = ws.split.parts;
     p.part = reinterpret_cast<float*>(wsp + ws.part_off);
   }
-  if ((int64_t)p.bh * nq + 8 * sage::kResidentWGs > 0x7fffffff)
+  if ((int64_t)p.bh * nq + 8 * sage::kResidentWGs > kMaxGridUnits)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(p.bh * nq));
   p.s_dump = s_dump;
   hipError_t e = sage::launch_attn(qk_kind, pv_kind, granularity, mask, p, d, (int)b, stream);
@@ -426,8 +435,12 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
     mask |= 1;
   }
   if (doc_ids) mask |= 2;
-  if ((b * h) * ((n + 127) / 128) > 0x7fffffff)
+  // the dK/dV and dQ launches: 512-thread workgroups, one per 128-row tile
+  if ((b * h) * ((n + 127) / 128) > kMaxGridUnits / 2)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(b * h * ((n + 127) / 128)));
+  if (sage::quant_grid_units(b * h, n, d) > kMaxGridUnits)
+    return fail(SAGE_ERR_ARG, "quantizing b*h=%lld x n=%lld exceeds one launch's %lld workgroups", (long long)(b * h),
+                (long long)n, (long long)kMaxGridUnits);
   const BwdWorkspace ws = bwd_workspace(b, b * h, n, d);
   if (!workspace || workspace_bytes < ws.bytes)
     return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", ws.bytes, workspace_bytes);

@@ -108,6 +108,7 @@ hipError_t launch_qkv_postprocess(const ProdArgs& prod, int64_t bh, int64_t n, i
 hipError_t launch_qkv_postprocess_bwd(const ProdArgs& prod, int64_t bh, int64_t n, int64_t d, const uint16_t* gq,
                                       const uint16_t* gk, const uint16_t* gv, uint16_t* dqkv, hipStream_t st);
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
+int64_t quant_grid_units(int64_t bh, int64_t n, int64_t d);
 
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb, hipStream_t st);
 // Per-batch document-id summaries (min doc, max doc, #valid, #padding) of every

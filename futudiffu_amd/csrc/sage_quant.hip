@@ -10,14 +10,23 @@
 // loop; per-token scales depend only on the token, so quantizing once here
 // yields identical codes.
 //
-// With smoothing, k_colsum first reads K once and writes fp64 column sums of
-// each 256-token chunk (no atomics, nothing to clear beforehand).  quantize
-// (one workgroup per 64-token block and head) then issues all of its Q, K and
-// V loads up front, adds the chunk sums of its head in a fixed order to form
-// the mean, and writes the Q, K and V codes.  The mean makes the second read
-// of K unavoidable: every K code depends on all N tokens.
+// Every workgroup has one role: the fp64 column sums of one K chunk (for the
+// smoothing mean), or the Q, V or K codes of one 64-token block of one head.
+// Rows past N are read through buffer resources, which return zeros.  With
+// smoothing the mean makes a second read of K unavoidable (every K code
+// depends on all N tokens); one kernel (quantize_one_kernel) dispatches the
+// column sums first and the K blocks last, which wait for their head's sums
+// through flags tagged with a per-call epoch.  Under stream capture the
+// launch uses two kernels instead (quantize_qv_kernel, quantize_k_kernel):
+// a captured epoch would repeat on every replay.  Both forms write the same
+// bits.
 #include "sage_common.h"
 #include "sage_launch.h"
+
+#include <atomic>
+#include <chrono>
+#include <cstdlib>
+#include <cstring>
 
 namespace sage {
 
@@ -33,21 +42,25 @@ __device__ __forceinline__ void unpack8(uint4 w, float x[8]) {
 
 // Max over aligned groups of G lanes (G in {8, 16}) with DPP row permutes:
 // quad xor 1, quad xor 2, half-row mirror (8 lanes), row mirror (16 lanes).
+// The operands are non-negative and not NaN, so their bit patterns order like
+// their values: an integer max fuses with the permute into one instruction.
 template <int G>
 __device__ __forceinline__ float group_max(float a) {
-  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xf, 0xf, false)));  // [1,0,3,2]
-  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xf, 0xf, false)));  // [2,3,0,1]
-  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x141, 0xf, 0xf, false)));  // half mirror
-  if constexpr (G == 16) a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x140, 0xf, 0xf, false)));
-  return a;
+  uint32_t u = __float_as_uint(a);
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xf, 0xf, true));   // [1,0,3,2]
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x4E, 0xf, 0xf, true));   // [2,3,0,1]
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x141, 0xf, 0xf, true));  // half mirror
+  if constexpr (G == 16) u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x140, 0xf, 0xf, true));
+  return __uint_as_float(u);
 }
 
-// Max across the 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
+// Max across the 16-lane rows of a wave (lanes l, l^16, l^32, l^48), for
+// non-negative, non-NaN operands (integer max of the bit patterns).
 __device__ __forceinline__ float rows_max(float a) {
   const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
-  a = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
-  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
-  return fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+  const uint32_t m = max((uint32_t)s16[0], (uint32_t)s16[1]);
+  const auto s32 = __builtin_amdgcn_permlane32_swap(m, m, false, false);
+  return __uint_as_float(max((uint32_t)s32[0], (uint32_t)s32[1]));
 }
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -56,19 +69,42 @@ __device__ __forceinline__ uint32_t word_of(uint4 w, int i) {
   return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
 }
 
+// Lane p of each quad, broadcast to the quad (p a constant after unrolling).
+template <int P>
+__device__ __forceinline__ float quad_lane_c(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), P * 0x55, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float quad_lane(float x, int p) {
+  return p == 0 ? quad_lane_c<0>(x) : p == 1 ? quad_lane_c<1>(x) : p == 2 ? quad_lane_c<2>(x) : quad_lane_c<3>(x);
+}
+
 // Quantize the 8 channels a lane holds for each of its PASSES tokens of one
 // operand (Q or K) and store codes in row-fragment order plus scales.
-// x holds the (smoothed) values; amax is per token, or per 64-token block.
+// x holds the (smoothed) values; amax is per token, or per 64-token block, and
+// the same in every lane of a token.  The correctly rounded divisions
+// qmax / amax and amax / qmax are formed once per quad: lane c8 (mod 4) works
+// for pass c8 % PASSES, and a quad permute hands every lane the result of
+// each pass.  Lane c8 = ps stores token ps's scale.
 template <int D, int QK, int GRAN, int PASSES>
 __device__ __forceinline__ void store_rows(const float (&x)[PASSES][8], const float (&amax)[PASSES], int64_t tok0,
                                            int rr, int c8, float fold, uint8_t* __restrict__ codes,
                                            float* __restrict__ scale, int tid) {
   constexpr int RPP = 256 / (D / 8);
+  static_assert(PASSES == 2 || PASSES == 4, "passes per quad");
   const float qmax = (QK == kQK_INT8) ? kInt8Max : kFp8Max;
+  // this lane's pass, selected with bit masks (a select chain would become
+  // an indexed array in LDS)
+  const int mine = c8 & (PASSES - 1);
+  uint32_t amb = 0u;
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) amb |= __float_as_uint(amax[ps]) & (0u - (uint32_t)(mine == ps));
+  const float am = __uint_as_float(amb);
+  const float inv_mine = qmax / fmaxf(am, kEps);  // IEEE division (correctly rounded)
+  const float scale_mine = (am / qmax) * fold;
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
     const int64_t tok = tok0 + rr + ps * RPP;
-    const float inv = qmax / fmaxf(amax[ps], kEps);  // IEEE division (correctly rounded)
+    const float inv = quad_lane(inv_mine, ps);
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = x[ps][e] * inv;
@@ -83,9 +119,9 @@ __device__ __forceinline__ void store_rows(const float (&x)[PASSES][8], const fl
     const int d0 = c8 * 8;
     *reinterpret_cast<uint2*>(codes + row_frag_offset(tok, d0 / 32, (d0 / 16) & 1, D) + (d0 & 8)) = word;
     if (GRAN == kGRAN_TOKEN) {
-      if (c8 == 0) scale[tok] = (amax[ps] / qmax) * fold;
+      if (c8 == ps) scale[tok] = scale_mine;
     } else if (tid == 0 && ps == 0) {
-      scale[tok0 / 64] = (amax[ps] / qmax) * fold;
+      scale[tok0 / 64] = scale_mine;
     }
   }
 }
@@ -365,197 +401,167 @@ __global__ void __launch_bounds__(256) qkv_postprocess_bwd_kernel(ProdArgs prod,
   }
 }
 
-// Tokens per K column-sum chunk.
-constexpr int kSumTokens = 256;
-
-__host__ __device__ inline int64_t k_sum_chunks(int64_t n) { return (n + kSumTokens - 1) / kSumTokens; }
-
-// Smoothing pass 1: fp64 column sums of K over each 256-token chunk of each
-// head, part[bh][chunk][d].  One workgroup per (chunk, bh); lane (rr, c8)
-// holds channels [8*c8, +8) of tokens rr + RPP*ps.  Every sum is formed in a
-// fixed order, so the result does not depend on scheduling.  PROD: K comes
-// from the projection output through the producer (RMSNorm + rotary), four
-// tokens per lane at a time.
-template <int D, bool PROD>
-__global__ void __launch_bounds__(256) k_colsum_kernel(const uint16_t* __restrict__ k, int64_t n,
-                                                       double* __restrict__ part, ProdArgs prod) {
-  constexpr int LPR = D / 8;
-  constexpr int RPP = 256 / LPR;
-  constexpr int PASSES = kSumTokens / RPP;
-  constexpr int GROUP = PROD ? 4 : PASSES;  // tokens per lane loaded together
-  __shared__ double ksw[4][D];
-  int64_t ch;
-  int bh;
-  block_coords<PROD>(prod, ch, bh);
-  const int tid = threadIdx.x, wave = tid >> 6;
-  const int c8 = tid % LPR, rr = tid / LPR;
-  const int64_t tok0 = (int64_t)ch * kSumTokens;
-  const HeadRows<D, PROD> src(k, k, k, prod, bh, n);
-  float kn[8];
-  if constexpr (PROD) load_w8(prod.kw, c8, kn);
-  double cs[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) cs[e] = 0.0;
-#pragma unroll 1
-  for (int g0 = 0; g0 < PASSES; g0 += GROUP) {
-    uint4 w[GROUP];
-#pragma unroll
-    for (int i = 0; i < GROUP; ++i) {
-      const int64_t tok = min(tok0 + rr + (g0 + i) * RPP, n - 1);  // clamped in bounds, masked below
-      w[i] = *reinterpret_cast<const uint4*>(src.k + tok * src.stride + c8 * 8);
-    }
-    if constexpr (PROD) {
-#pragma unroll
-      for (int i = 0; i < GROUP; ++i) {
-        f32x4 fr[4];
-        load_freqs<D>(prod.freqs, src.row0 + min(tok0 + rr + (g0 + i) * RPP, n - 1), c8, fr);
-        w[i] = rms_rope8<D>(w[i], kn, fr, prod.eps);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < GROUP; ++i) {
-      float x[8];
-      unpack8(w[i], x);
-      const bool keep = tok0 + rr + (g0 + i) * RPP < n;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) cs[e] += keep ? (double)x[e] : 0.0;
-    }
-  }
-  // token rows of the wave (lanes c8 + LPR*m), then the 4 waves
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) cs[e] += __shfl_xor(cs[e], off);
-  if ((tid & 63) < LPR) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ksw[wave][c8 * 8 + e] = cs[e];
-  }
-  __syncthreads();
-  if (tid < D)
-    part[((int64_t)bh * k_sum_chunks(n) + ch) * D + tid] = (ksw[0][tid] + ksw[1][tid]) + (ksw[2][tid] + ksw[3][tid]);
+// K column sums: each head's tokens form at most kMaxChunks(D) chunks of a
+// multiple of 256 tokens, so the quantization reads every chunk sum of a head
+// in one round of loads (kMeanLoads per thread, 256 / D threads per channel).
+constexpr int kMeanLoads = 12;
+__host__ __device__ constexpr int k_max_chunks(int64_t d) { return kMeanLoads * (int)(256 / d); }
+__host__ __device__ inline int64_t k_sum_tokens(int64_t n, int64_t d) {
+  const int64_t c256 = (n + 255) / 256;
+  return 256 * ((c256 + k_max_chunks(d) - 1) / k_max_chunks(d));
+}
+__host__ __device__ inline int64_t k_sum_chunks(int64_t n, int64_t d) {
+  const int64_t t = k_sum_tokens(n, d);
+  return (n + t - 1) / t;
 }
 
-// One workgroup per (64-token block, bh).
-//   Q, K: lane (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps.
-//   V:    lane (g, c8) holds channels [8*c8, +8) of the 4 consecutive tokens
-//         4g..4g+3, so the 4 codes of a channel form one 32-bit fragment word.
-// With smoothing, the head's mean is the sum of its chunk sums (fixed order)
-// / N in fp64, rounded to fp32 then bf16 (the reference's bf16 mean), and K
-// rows are smoothed as bf16(k - mean).  PROD: q, k and v come from the
-// projection output, q and k through the producer (RMSNorm + rotary), so the
-// codes equal those of the producer's bf16 outputs.
-template <int D, int QK, int PV, int GRAN, bool SMOOTH, bool PROD>
-__global__ void __launch_bounds__(256) quantize_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    int64_t n, int64_t np, float fold, const double* __restrict__ ksum_part,
-    uint8_t* __restrict__ qc, float* __restrict__ qs, uint8_t* __restrict__ kc, float* __restrict__ ks,
-    uint8_t* __restrict__ vout, float* __restrict__ vs, uint16_t* __restrict__ kmean, ProdArgs prod) {
+// Buffer resource over rows [tok0, tok0 + rows) of one head's source (tokens
+// `stride` elements apart, D channels each).  Loads past the last valid row
+// return zeros, so tokens past N need neither clamping nor masking.
+template <int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const uint16_t* src, int64_t stride, int64_t tok0,
+                                                            int64_t n, int rows) {
+  const int64_t nv = min((int64_t)rows, n - tok0);
+  const uint32_t bytes = nv > 0 ? (uint32_t)(((nv - 1) * stride + D) * 2) : 0u;
+  return raw_rsrc(src + tok0 * stride, bytes);
+}
+
+// 16 bytes at byte offset voff (whole offset in the VGPR: the range check
+// covers it), zeros when out of range.
+__device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t rs, uint32_t voff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, 0, 0));
+}
+
+// LDS of the quantization workgroups, one role at a time (byte offsets).
+template <int D, int PV>
+struct QuantLds {
+  static constexpr int kVmax = 0;                  // float [4][D]: V channel maxima per wave
+  static constexpr int kInv = kVmax + 4 * D * 4;   // float [D]: V inverse scales
+  static constexpr int kImg = kInv + D * 4;        // V operand image of the block
+  static constexpr int kBytes = kImg + (PV == kPV_FP8 ? 1 : 2) * 64 * D;
+  // K column sums: double [4][D] from offset 0; Q/K block amax: 2 words at the end
+  static constexpr int kAmax = kBytes;
+  static constexpr int kTotal = kAmax + 16;
+  static_assert(4 * D * 8 <= kBytes, "column-sum scratch fits");
+};
+
+// Issue the 16-byte loads of a lane's tokens of one 64-token block: lane
+// (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps.  Rows past N read
+// as zeros.
+template <int D>
+__device__ __forceinline__ void rows_load(const uint16_t* src, int64_t stride, int64_t tok0, int64_t n, int tid,
+                                          uint4 (&w)[64 / (256 / (D / 8))]) {
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   constexpr int PASSES = 64 / RPP;
-  constexpr int VTHREADS = 16 * LPR;  // 16 groups of 4 tokens
-  __shared__ unsigned int blk_amax[2];
-  __shared__ __attribute__((aligned(16))) float vmax[4][D];
-  // smoothing: the TPC threads of a column each sum every TPC-th chunk sum
-  constexpr int TPC = 256 / D;
-  constexpr int kMeanLoads = 12;  // chunk sums in flight per thread
-  __shared__ double msum[SMOOTH ? TPC : 1][D];
-  __shared__ float mu[SMOOTH ? D : 1];
-  // V operand image of this 64-token block in fragment order; written to
-  // global as contiguous 16-byte chunks
-  __shared__ __attribute__((aligned(16))) uint8_t vimg[(PV == kPV_FP8 ? 1 : 2) * 64 * D];
-  int64_t blk;
-  int bh;
-  block_coords<PROD>(prod, blk, bh);
-  const int tid = threadIdx.x, wave = tid >> 6;
   const int c8 = tid % LPR, rr = tid / LPR;
-  const int64_t tok0 = (int64_t)blk * 64;
-  const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
-  const int64_t co = (int64_t)bh * np * D;
-  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
-
-  if (tid < 2) blk_amax[tid] = 0u;
-  __syncthreads();
-
-  // ---- smoothing: this thread's chunk sums, loaded before the block's data ----
-  // Thread (j = tid / D, column tid % D) adds chunks j, j + TPC, ... in order.
-  const int64_t nch = SMOOTH ? k_sum_chunks(n) : 0;
-  const double* pp = ksum_part + ((int64_t)bh * nch + tid / D) * D + tid % D;
-  double mt[SMOOTH ? kMeanLoads : 1];
-  if constexpr (SMOOTH) {
+  const __amdgpu_buffer_rsrc_t rs = rows_rsrc<D>(src, stride, tok0, n, 64);
 #pragma unroll
-    for (int i = 0; i < kMeanLoads; ++i) mt[i] = tid / D + TPC * i < nch ? pp[(int64_t)TPC * i * D] : 0.0;
-  }
+  for (int ps = 0; ps < PASSES; ++ps) w[ps] = load16(rs, (uint32_t)(((rr + ps * RPP) * stride + c8 * 8) * 2));
+}
 
-  // ---- issue every load of the block up front ------------------------------
-  // Token indices are clamped to N-1 so every load is in bounds and issued
-  // without branches; values of tokens past N are zeroed afterwards.
-  uint4 qw[PASSES], kw[PASSES], vw[4];
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
-#pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) {
-    const int64_t tok = min(tok0 + rr + ps * RPP, n - 1);
-    qw[ps] = *reinterpret_cast<const uint4*>(src.q + tok * src.stride + c8 * 8);
-    kw[ps] = *reinterpret_cast<const uint4*>(src.k + tok * src.stride + c8 * 8);
-  }
-  const int g = (tid / LPR) & 15;  // V token group (V work only for tid < VTHREADS)
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t tok = min(tok0 + 4 * g + i, n - 1);
-    vw[i] = *reinterpret_cast<const uint4*>(src.v + tok * src.stride + c8 * 8);
-  }
+// Q, or K without smoothing (mu == nullptr), or K smoothed by the head's bf16
+// mean mu[D] (in LDS): codes in row-fragment order and scales of one 64-token
+// block from the loads of rows_load.  PROD: rows of the projection output
+// through RMSNorm + rotary (weights nw).  TAIL: the block reaches past N.
+template <int D, int QK, int GRAN, bool PROD, bool TAIL>
+__device__ __forceinline__ void rows_quant(uint4 (&w)[64 / (256 / (D / 8))], int64_t row0, const float* nw,
+                                           const ProdArgs& prod, int64_t tok0, int64_t n, float fold,
+                                           const float* mu, uint8_t* __restrict__ codes, float* __restrict__ scale,
+                                           unsigned* blk_amax, int tid) {
+  constexpr int LPR = D / 8;
+  constexpr int RPP = 256 / LPR;
+  constexpr int PASSES = 64 / RPP;
+  const int c8 = tid % LPR, rr = tid / LPR;
   if constexpr (PROD) {
-    // the producer's bf16 q and k (every lane of a token takes part in its sum)
-    float qn[8], kn[8];
-    load_w8(prod.qw, c8, qn);
-    load_w8(prod.kw, c8, kn);
+    float wn[8];
+    load_w8(nw, c8, wn);
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
       f32x4 fr[4];
-      load_freqs<D>(prod.freqs, src.row0 + min(tok0 + rr + ps * RPP, n - 1), c8, fr);
-      qw[ps] = rms_rope8<D>(qw[ps], qn, fr, prod.eps);
-      kw[ps] = rms_rope8<D>(kw[ps], kn, fr, prod.eps);
+      load_freqs<D>(prod.freqs, row0 + min(tok0 + rr + ps * RPP, n - 1), c8, fr);
+      w[ps] = rms_rope8<D>(w[ps], wn, fr, prod.eps);
+      if (tok0 + rr + ps * RPP >= n) w[ps] = make_uint4(0, 0, 0, 0);  // +0 codes past N
+    }
+  }
+  float x[PASSES][8], amax[PASSES];
+  float m[8];
+  if (mu != nullptr) {
+    const f32x4* m4 = reinterpret_cast<const f32x4*>(mu + c8 * 8);
+    const f32x4 a = m4[0], b = m4[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m[i] = a[i];
+      m[4 + i] = b[i];
     }
   }
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
-    if (tok0 + rr + ps * RPP >= n) {
-      qw[ps] = zero4;
-      kw[ps] = zero4;
+    unpack8(w[ps], x[ps]);
+    if (mu != nullptr) {
+      // bf16(k - mean); rows past N (loaded as zeros) stay zero
+      const float keep = (!TAIL || tok0 + rr + ps * RPP < n) ? 1.0f : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const uint32_t p2 = pack_bf16x2(x[ps][e] - m[e], x[ps][e + 1] - m[e + 1]);  // round to nearest even
+        x[ps][e] = __uint_as_float(p2 << 16);
+        x[ps][e + 1] = __uint_as_float(p2 & 0xffff0000u);
+        if constexpr (TAIL) {
+          x[ps][e] *= keep;
+          x[ps][e + 1] *= keep;
+        }
+      }
     }
   }
+  row_amax<D, GRAN, PASSES>(x, amax, blk_amax);
+  store_rows<D, QK, GRAN, PASSES>(x, amax, tok0, rr, c8, fold, codes, scale, tid);
+}
+
+template <int D, int QK, int GRAN, bool PROD>
+__device__ __forceinline__ void rows_block(const uint16_t* src, int64_t stride, int64_t row0, const float* nw,
+                                           const ProdArgs& prod, int64_t tok0, int64_t n, float fold,
+                                           uint8_t* __restrict__ codes, float* __restrict__ scale, unsigned* blk_amax,
+                                           int tid) {
+  uint4 w[64 / (256 / (D / 8))];
+  rows_load<D>(src, stride, tok0, n, tid, w);
+  rows_quant<D, QK, GRAN, PROD, false>(w, row0, nw, prod, tok0, n, fold, nullptr, codes, scale, blk_amax, tid);
+}
+
+// V of one 64-token block: per-channel fp8 scales and codes, or bf16, in the
+// P.V operand's fragment order.  Lane (g, c8) holds channels [8*c8, +8) of the
+// 4 consecutive tokens 4g..4g+3, so the 4 codes of a channel form one 32-bit
+// fragment word.  The image is assembled in LDS and written as contiguous
+// 16-byte chunks.
+template <int D, int PV>
+__device__ __forceinline__ void v_block(const uint16_t* src, int64_t stride, int64_t tok0, int64_t n, int64_t blk,
+                                        int bh, int64_t np, uint8_t* __restrict__ vout, float* __restrict__ vs,
+                                        uint8_t* lds, int tid) {
+  constexpr int LPR = D / 8;
+  constexpr int VTHREADS = 16 * LPR;  // 16 groups of 4 tokens
+  constexpr int VW = VTHREADS / 64;   // waves holding V
+  using L = QuantLds<D, PV>;
+  float* vmax = reinterpret_cast<float*>(lds + L::kVmax);
+  float* vinv = reinterpret_cast<float*>(lds + L::kInv);
+  uint8_t* vimg = lds + L::kImg;
+  const int wave = tid >> 6, c8 = tid % LPR;
+  const int g = (tid / LPR) & 15;
+  const __amdgpu_buffer_rsrc_t rs = rows_rsrc<D>(src, stride, tok0, n, 64);
+  uint4 vw[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    if (tid >= VTHREADS || tok0 + 4 * g + i >= n) vw[i] = zero4;
-  if constexpr (SMOOTH) {
-    double s = 0.0;
-#pragma unroll
-    for (int i = 0; i < kMeanLoads; ++i) s += mt[i];
-    for (int64_t c = tid / D + TPC * kMeanLoads; c < nch; c += TPC) s += pp[(c - tid / D) * D];  // long heads
-    msum[tid / D][tid % D] = s;  // combined after the V section's barrier
-  }
-  // ---- Q -----------------------------------------------------------------------
-  {
-    float x[PASSES][8], amax[PASSES];
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) unpack8(qw[ps], x[ps]);
-    row_amax<D, GRAN, PASSES>(x, amax, &blk_amax[0]);
-    store_rows<D, QK, GRAN, PASSES>(x, amax, tok0, rr, c8, fold, qc + co, qs + sco, tid);
-  }
-
-  // ---- V -------------------------------------------------------------------------
-  if (PV == kPV_FP8) {
-    // channel maxima of |v| over the 4 tokens, on the bf16 bit patterns: for
-    // non-NaN values the magnitude bits order like the magnitudes, and the
-    // 32 unpacked floats need not stay live across the barrier below
+    vw[i] = tid < VTHREADS ? load16(rs, (uint32_t)(((4 * g + i) * stride + c8 * 8) * 2)) : make_uint4(0, 0, 0, 0);
+  const int64_t co = (int64_t)bh * np * D;
+  if constexpr (PV == kPV_FP8) {
+    // channel maxima of |v| over the 4 tokens, on the bf16 bit patterns (for
+    // non-NaN values the magnitude bits order like the magnitudes)
     float cm[8];
 #pragma unroll
     for (int w4 = 0; w4 < 4; ++w4) {
-      u16x2 m = __builtin_bit_cast(u16x2, word_of(vw[0], w4) & 0x7fff7fffu);
+      u16x2 mm = __builtin_bit_cast(u16x2, word_of(vw[0], w4) & 0x7fff7fffu);
 #pragma unroll
-      for (int i = 1; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, word_of(vw[i], w4) & 0x7fff7fffu));
-      cm[2 * w4] = __uint_as_float((uint32_t)m.x << 16);
-      cm[2 * w4 + 1] = __uint_as_float((uint32_t)m.y << 16);
+      for (int i = 1; i < 4; ++i) mm = __builtin_elementwise_max(mm, __builtin_bit_cast(u16x2, word_of(vw[i], w4) & 0x7fff7fffu));
+      cm[2 * w4] = __uint_as_float((uint32_t)mm.x << 16);
+      cm[2 * w4 + 1] = __uint_as_float((uint32_t)mm.y << 16);
     }
     // across the token groups of this wave (lanes c8 + LPR*m), then across waves
 #pragma unroll
@@ -566,39 +572,30 @@ __global__ void __launch_bounds__(256) quantize_kernel(
       cm[e] = rows_max(cm[e]);
     }
     if (tid < VTHREADS && (tid & 63) < LPR) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vmax[wave][c8 * 8 + e] = cm[e];
+      f32x4* o4 = reinterpret_cast<f32x4*>(vmax + wave * D + c8 * 8);
+      o4[0] = f32x4{cm[0], cm[1], cm[2], cm[3]};
+      o4[1] = f32x4{cm[4], cm[5], cm[6], cm[7]};
     }
     __syncthreads();
-    constexpr int VW = VTHREADS / 64;  // waves holding V
+    // one thread per channel: the block's maximum, its scale and inverse
+    if (tid < D) {
+      float am = vmax[tid];
+#pragma unroll
+      for (int ww = 1; ww < VW; ++ww) am = fmaxf(am, vmax[ww * D + tid]);
+      vinv[tid] = kFp8Max / fmaxf(am, kEps);
+      vs[((int64_t)bh * (np / 64) + blk) * D + tid] = am / kFp8Max;
+    }
+    __syncthreads();
     if (tid < VTHREADS) {
-      float am[8];
+      float inv[8];
       {
-        const f32x4* v4 = reinterpret_cast<const f32x4*>(&vmax[0][c8 * 8]);
-        const f32x4 a0 = v4[0], a1 = v4[1];
+        const f32x4* i4 = reinterpret_cast<const f32x4*>(vinv + c8 * 8);
+        const f32x4 a = i4[0], b = i4[1];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          am[i] = a0[i];
-          am[4 + i] = a1[i];
+          inv[i] = a[i];
+          inv[4 + i] = b[i];
         }
-#pragma unroll
-        for (int ww = 1; ww < VW; ++ww) {
-          const f32x4* w4 = reinterpret_cast<const f32x4*>(&vmax[ww][c8 * 8]);
-          const f32x4 b0 = w4[0], b1 = w4[1];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            am[i] = fmaxf(am[i], b0[i]);
-            am[4 + i] = fmaxf(am[4 + i], b1[i]);
-          }
-        }
-      }
-      float inv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) inv[e] = kFp8Max / fmaxf(am[e], kEps);
-      if (g == 0) {
-        f32x4* o4 = reinterpret_cast<f32x4*>(vs + ((int64_t)bh * (np / 64) + blk) * D + c8 * 8);
-        o4[0] = f32x4{am[0] / kFp8Max, am[1] / kFp8Max, am[2] / kFp8Max, am[3] / kFp8Max};
-        o4[1] = f32x4{am[4] / kFp8Max, am[5] / kFp8Max, am[6] / kFp8Max, am[7] / kFp8Max};
       }
       // word of channel d = 32j + r for tokens 4g..4g+3 -> chunk (j, b, L = 32h + r), byte 4jj,
       // with g = 8b + 2jj + h
@@ -634,41 +631,363 @@ __global__ void __launch_bounds__(256) quantize_kernel(
     }
   }
   __syncthreads();
-  if constexpr (SMOOTH) {
-    if (tid < D) {
-      double s = msum[0][tid];
+  constexpr int VBYTES = (PV == kPV_FP8 ? 1 : 2) * 64 * D;
+  uint8_t* vo = vout + (PV == kPV_FP8 ? 1 : 2) * (co + tok0 * D);
 #pragma unroll
-      for (int j = 1; j < TPC; ++j) s += msum[j][tid];
-      const uint16_t m16 = f32_to_bf16_rne((float)(s / (double)n));
-      mu[tid] = bf16_to_f32(m16);
-      if (blk == 0) kmean[(int64_t)bh * D + tid] = m16;
-    }
-  }
-  {
-    constexpr int VBYTES = (PV == kPV_FP8 ? 1 : 2) * 64 * D;
-    uint8_t* vo = vout + (PV == kPV_FP8 ? 1 : 2) * (co + tok0 * D);
-#pragma unroll
-    for (int i = tid; i < VBYTES / 16; i += 256)
-      reinterpret_cast<uint4*>(vo)[i] = reinterpret_cast<const uint4*>(vimg)[i];
-  }
-  if constexpr (SMOOTH) __syncthreads();  // mu
+  for (int i = tid; i < VBYTES / 16; i += 256)
+    reinterpret_cast<uint4*>(vo)[i] = reinterpret_cast<const uint4*>(vimg)[i];
+}
 
-  // ---- K ---------------------------------------------------------------------
-  {
-    float x[PASSES][8], amax[PASSES];
+// fp64 column sums of K over one chunk (k_sum_tokens tokens) of one head.
+// Lane (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps; the lanes of
+// a column are added in a fixed tree, then the 4 waves through ksw (LDS,
+// 4 * D doubles).  Returns the chunk's sum of column tid for tid < D (after a
+// workgroup barrier; callers synchronize again before reusing ksw).  Every
+// sum is formed in a fixed order, so the result does not depend on
+// scheduling or on which workgroup computes it.
+template <int D, bool PROD, int GROUP = (PROD ? 4 : 8)>
+__device__ __forceinline__ double chunk_colsum(const uint16_t* src, int64_t stride, int64_t row0, const ProdArgs& prod,
+                                               int64_t ch, int64_t n, double* ksw, int tid) {
+  constexpr int LPR = D / 8;
+  constexpr int RPP = 256 / LPR;
+  // GROUP: tokens per lane loaded together
+  const int wave = tid >> 6, c8 = tid % LPR, rr = tid / LPR;
+  const int64_t ct = k_sum_tokens(n, D);
+  const int64_t tok0 = ch * ct;
+  float kn[8];
+  if constexpr (PROD) load_w8(prod.kw, c8, kn);
+  double cs[8];
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      unpack8(kw[ps], x[ps]);
-      if constexpr (SMOOTH) {
-        // rows past N were loaded as zeros; keep them zero after the shift
-        const float keep = tok0 + rr + ps * RPP < n ? 1.0f : 0.0f;
+  for (int e = 0; e < 8; ++e) cs[e] = 0.0;
+  // 256-token pieces (one buffer resource each: 32-bit offsets), GROUP rows per lane at a time
+#pragma unroll 1
+  for (int64_t t0 = tok0; t0 < min(tok0 + ct, n); t0 += 256) {
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc<D>(src, stride, t0, n, 256);
+#pragma unroll 1
+    for (int g0 = 0; g0 < 256 / RPP; g0 += GROUP) {
+      uint4 w[GROUP];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[ps][e] = bf16_to_f32(f32_to_bf16_rne(x[ps][e] - mu[c8 * 8 + e])) * keep;
+      for (int i = 0; i < GROUP; ++i) w[i] = load16(rs, (uint32_t)(((rr + (g0 + i) * RPP) * stride + c8 * 8) * 2));
+      if constexpr (PROD) {
+#pragma unroll
+        for (int i = 0; i < GROUP; ++i) {
+          f32x4 fr[4];
+          load_freqs<D>(prod.freqs, row0 + min(t0 + rr + (g0 + i) * RPP, n - 1), c8, fr);
+          w[i] = rms_rope8<D>(w[i], kn, fr, prod.eps);  // zero rows stay zero
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < GROUP; ++i) {
+        float x[8];
+        unpack8(w[i], x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cs[e] += (double)x[e];
       }
     }
-    row_amax<D, GRAN, PASSES>(x, amax, &blk_amax[1]);
-    store_rows<D, QK, GRAN, PASSES>(x, amax, tok0, rr, c8, 1.0f, kc + co, ks + sco, tid);
   }
+  // token rows of the wave (lanes c8 + LPR*m), then the 4 waves
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) cs[e] += __shfl_xor(cs[e], off);
+  if ((tid & 63) < LPR) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ksw[wave * D + c8 * 8 + e] = cs[e];
+  }
+  __syncthreads();
+  return tid < D ? (ksw[tid] + ksw[D + tid]) + (ksw[2 * D + tid] + ksw[3 * D + tid]) : 0.0;
+}
+
+// The head mean of the smoothing, mu[D] in LDS (fp32 of the bf16 mean), from
+// the head's chunk sums: thread j = tid / D of column tid % D adds chunks j,
+// j + TPC, ... in order (mt: its kMeanLoads loaded sums, zero past nch), then
+// the TPC partial sums of a column are added in order; / N in fp64, rounded
+// to fp32 then bf16 (the reference's bf16 mean).  kmean: written when not null.
+template <int D>
+__device__ __forceinline__ void head_mean(double s, int64_t n, double (*msum)[D], float* mu, uint16_t* kmean,
+                                          int tid) {
+  constexpr int TPC = 256 / D;
+  msum[tid / D][tid % D] = s;
+  __syncthreads();
+  if (tid < D) {
+    double t = msum[0][tid];
+#pragma unroll
+    for (int j = 1; j < TPC; ++j) t += msum[j][tid];
+    const uint16_t m16 = f32_to_bf16_rne((float)(t / (double)n));
+    mu[tid] = bf16_to_f32(m16);
+    if (kmean != nullptr) kmean[tid] = m16;
+  }
+  __syncthreads();
+}
+
+// Loads of the head's chunk sums for head_mean (clamped in bounds so they
+// issue without branches; values past nch are dropped by mean_sum).
+template <int D, bool COHERENT = false>
+__device__ __forceinline__ void load_chunk_sums(const double* hp, int64_t nch, int tid, double (&mt)[kMeanLoads]) {
+  constexpr int TPC = 256 / D;
+#pragma unroll
+  for (int i = 0; i < kMeanLoads; ++i) {
+    const double* p = hp + min((int64_t)(tid / D + TPC * i), nch - 1) * D;
+    if constexpr (COHERENT)
+      mt[i] = __builtin_bit_cast(double, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT));
+    else
+      mt[i] = *p;
+  }
+}
+template <int D>
+__device__ __forceinline__ double mean_sum(const double (&mt)[kMeanLoads], int64_t nch, int tid) {
+  constexpr int TPC = 256 / D;
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < kMeanLoads; ++i) s += tid / D + TPC * i < nch ? mt[i] : 0.0;
+  return s;
+}
+
+// First quantization kernel of the two-kernel form: one role per workgroup,
+// 1D grid with every role of every head of the same rows adjacent.
+//   SMOOTH: units [0, nch * BH) the K column sums of chunk u / BH of head
+//           u % BH; then unit 2 * (blk * BH + head) + role, role 0 = Q, 1 = V.
+//   else:   unit 3 * (blk * BH + head) + role, role 2 = K.
+// The longest workgroups (column sums) are dispatched first, and the short
+// block roles fill the CUs around them.
+template <int D, int QK, int PV, int GRAN, bool SMOOTH, bool PROD>
+__global__ void __launch_bounds__(256) quantize_qv_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t bhn,
+    int64_t n, int64_t np, float fold, double* __restrict__ ksum_part, uint8_t* __restrict__ qc,
+    float* __restrict__ qs, uint8_t* __restrict__ kc, float* __restrict__ ks, uint8_t* __restrict__ vout,
+    float* __restrict__ vs, ProdArgs prod) {
+  using L = QuantLds<D, PV>;
+  constexpr int ROLES = SMOOTH ? 2 : 3;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kTotal];
+  unsigned* blk_amax = reinterpret_cast<unsigned*>(lds + L::kAmax);
+  const int tid = threadIdx.x;
+  int64_t u = blockIdx.x;
+  if constexpr (SMOOTH) {
+    const int64_t nch = k_sum_chunks(n, D), nsum = nch * bhn;
+    if (u < nsum) {
+      const int64_t ch = u / bhn;
+      const int bh = (int)(u - ch * bhn);
+      const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+      const double cs = chunk_colsum<D, PROD>(src.k, src.stride, src.row0, prod, ch, n,
+                                              reinterpret_cast<double*>(lds), tid);
+      if (tid < D) ksum_part[((int64_t)bh * nch + ch) * D + tid] = cs;
+      return;
+    }
+    u -= nsum;
+  }
+  const int role = (int)(u % ROLES);
+  const int64_t rest = u / ROLES;
+  const int64_t blk = rest / bhn;
+  const int bh = (int)(rest - blk * bhn);
+  const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+  const int64_t tok0 = blk * 64;
+  const int64_t co = (int64_t)bh * np * D;
+  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+  if (role == 1) {
+    v_block<D, PV>(src.v, src.stride, tok0, n, blk, bh, np, vout, vs, lds, tid);
+    return;
+  }
+  if (GRAN == kGRAN_BLOCK64) {
+    if (tid == 0) *blk_amax = 0u;
+    __syncthreads();
+  }
+  if (role == 0)
+    rows_block<D, QK, GRAN, PROD>(src.q, src.stride, src.row0, prod.qw, prod, tok0, n, fold, qc + co, qs + sco,
+                                  blk_amax, tid);
+  else
+    rows_block<D, QK, GRAN, PROD>(src.k, src.stride, src.row0, prod.kw, prod, tok0, n, 1.0f, kc + co, ks + sco,
+                                  blk_amax, tid);
+}
+
+// Second quantization kernel of the two-kernel form (smoothing): K of two
+// 64-token blocks of one head (the padded length is a multiple of 128),
+// shifted by the head's mean; 1D grid, unit y * BH + head.  The chunk sums
+// are loaded first (needed first), then the K rows.
+template <int D, int QK, int GRAN, bool PROD>
+__global__ void __launch_bounds__(256) quantize_k_kernel(const uint16_t* __restrict__ k, int64_t bhn, int64_t n,
+                                                         int64_t np, const double* __restrict__ ksum_part,
+                                                         uint8_t* __restrict__ kc, float* __restrict__ ks,
+                                                         uint16_t* __restrict__ kmean, ProdArgs prod) {
+  constexpr int TPC = 256 / D;
+  constexpr int PASSES = 64 / (256 / (D / 8));
+  __shared__ double msum[TPC][D];
+  __shared__ __attribute__((aligned(16))) float mu[D];
+  __shared__ unsigned blk_amax[2];
+  const int tid = threadIdx.x;
+  const int64_t y = blockIdx.x / bhn;
+  const int bh = (int)(blockIdx.x - y * bhn);
+  const int64_t tok0 = y * 128;
+  const HeadRows<D, PROD> src(k, k, k, prod, bh, n);
+  const int64_t nch = k_sum_chunks(n, D);  // at most kMeanLoads * TPC
+  double mt[kMeanLoads];
+  load_chunk_sums<D>(ksum_part + (int64_t)bh * nch * D + tid % D, nch, tid, mt);
+  uint4 w0[PASSES], w1[PASSES];
+  rows_load<D>(src.k, src.stride, tok0, n, tid, w0);
+  rows_load<D>(src.k, src.stride, tok0 + 64, n, tid, w1);
+  if (GRAN == kGRAN_BLOCK64 && tid < 2) blk_amax[tid] = 0u;
+  head_mean<D>(mean_sum<D>(mt, nch, tid), n, msum, mu, y == 0 ? kmean + (int64_t)bh * D : nullptr, tid);
+  const int64_t co = (int64_t)bh * np * D;
+  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+  if (tok0 + 128 <= n) {
+    rows_quant<D, QK, GRAN, PROD, false>(w0, src.row0, prod.kw, prod, tok0, n, 1.0f, mu, kc + co, ks + sco,
+                                         &blk_amax[0], tid);
+    rows_quant<D, QK, GRAN, PROD, false>(w1, src.row0, prod.kw, prod, tok0 + 64, n, 1.0f, mu, kc + co, ks + sco,
+                                         &blk_amax[1], tid);
+  } else {
+    rows_quant<D, QK, GRAN, PROD, true>(w0, src.row0, prod.kw, prod, tok0, n, 1.0f, mu, kc + co, ks + sco,
+                                        &blk_amax[0], tid);
+    rows_quant<D, QK, GRAN, PROD, true>(w1, src.row0, prod.kw, prod, tok0 + 64, n, 1.0f, mu, kc + co, ks + sco,
+                                        &blk_amax[1], tid);
+  }
+}
+
+// One-kernel form with smoothing (not used under stream capture: the epoch is
+// a launch argument).  1D grid, units in dispatch order:
+//   [0, nsum)   K column sums of chunk u / BH of head u % BH; each publishes
+//               flag[head][chunk] = epoch after its sums;
+//   then rows   the Q, V and K roles of the 64-token blocks, with the K block
+//               of row r - lag beside the Q and V blocks of row r (rows
+//               0..lag-1 carry only Q and V, the last lag rows only K): the
+//               column sums run well ahead of the first K block, and the K
+//               blocks overlap the Q/V stream instead of forming a tail.
+// Each K workgroup reads its head's flags and proceeds when every chunk shows
+// this call's epoch (a 64-bit value the host never reuses, so memory left by
+// earlier calls never matches).  The wait is bounded: after spin_limit rounds
+// the workgroup forms the chunk sums itself, with the same arithmetic and
+// order (chunk_colsum), so every workgroup exits and the codes are the same
+// either way.
+template <int D, int QK, int PV, int GRAN, bool PROD>
+__global__ void __launch_bounds__(256) quantize_one_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t bhn,
+    int64_t n, int64_t np, float fold, double* __restrict__ ksum_part, uint64_t* __restrict__ flags,
+    uint64_t epoch, int spin_limit, int64_t lag, uint8_t* __restrict__ qc, float* __restrict__ qs, uint8_t* __restrict__ kc,
+    float* __restrict__ ks, uint8_t* __restrict__ vout, float* __restrict__ vs, uint16_t* __restrict__ kmean,
+    ProdArgs prod) {
+  using L = QuantLds<D, PV>;
+  constexpr int TPC = 256 / D;
+  constexpr int PASSES = 64 / (256 / (D / 8));
+  static_assert(TPC * D * 8 + D * 4 + 4 * D * 8 <= L::kBytes, "K role scratch fits");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kTotal];
+  unsigned* blk_amax = reinterpret_cast<unsigned*>(lds + L::kAmax);
+  const int tid = threadIdx.x;
+  const int64_t nch = k_sum_chunks(n, D), nsum = nch * bhn;
+  const int64_t nblk = np / 64;
+  int64_t u = blockIdx.x;
+  if (u < nsum) {
+    const int64_t ch = u / bhn;
+    const int bh = (int)(u - ch * bhn);
+    const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+    const double cs = chunk_colsum<D, PROD>(src.k, src.stride, src.row0, prod, ch, n,
+                                            reinterpret_cast<double*>(lds), tid);
+    // The sums and the flag go out as agent-scope relaxed atomic stores, which
+    // gfx950 writes through to the device's coherence point (sc1); waiting for
+    // the sums' completion before the flag store orders them without the
+    // whole-L2 write-back of a release fence.
+    if (tid < D)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(ksum_part) + ((int64_t)bh * nch + ch) * D + tid,
+                         __builtin_bit_cast(uint64_t, cs), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vmem();
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(&flags[(int64_t)bh * nch + ch], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  u -= nsum;
+  // block roles with the K blocks `lag` rows behind the Q and V blocks
+  int role;
+  int64_t blk;
+  int bh;
+  const int64_t seg1 = 2 * bhn * lag, seg2 = 3 * bhn * (nblk - lag);
+  if (u < seg1) {
+    role = (int)(u & 1);
+    const int64_t rest = u >> 1;
+    blk = rest / bhn;
+    bh = (int)(rest - blk * bhn);
+  } else if (u < seg1 + seg2) {
+    const int64_t w = u - seg1;
+    role = (int)(w % 3);
+    const int64_t rest = w / 3;
+    const int64_t r = lag + rest / bhn;
+    bh = (int)(rest % bhn);
+    blk = role == 2 ? r - lag : r;
+  } else {
+    const int64_t w = u - seg1 - seg2;
+    role = 2;
+    blk = nblk - lag + w / bhn;
+    bh = (int)(w % bhn);
+  }
+  if (role != 2) {
+    const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+    const int64_t tok0 = blk * 64;
+    if (role == 1) {
+      v_block<D, PV>(src.v, src.stride, tok0, n, blk, bh, np, vout, vs, lds, tid);
+      return;
+    }
+    if (GRAN == kGRAN_BLOCK64) {
+      if (tid == 0) *blk_amax = 0u;
+      __syncthreads();
+    }
+    const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+    rows_block<D, QK, GRAN, PROD>(src.q, src.stride, src.row0, prod.qw, prod, tok0, n, fold,
+                                  qc + (int64_t)bh * np * D, qs + sco, blk_amax, tid);
+    return;
+  }
+  // ---- K of one block ----
+  double(*msum)[D] = reinterpret_cast<double(*)[D]>(lds);
+  float* mu = reinterpret_cast<float*>(lds + TPC * D * 8);
+  double* ksw = reinterpret_cast<double*>(lds + TPC * D * 8 + D * 4);
+  const int64_t tok0 = blk * 64;
+  const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+  const uint64_t* hf = flags + (int64_t)bh * nch;
+  // flags and sums are read with agent-scope relaxed atomic loads, which read
+  // the coherence point (sc1), issued only after the flags show this epoch
+  uint64_t f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+  if (GRAN == kGRAN_BLOCK64 && tid == 0) *blk_amax = 0u;
+  bool ready = __syncthreads_and(f == epoch);
+  for (int r = 0; !ready && r < spin_limit; ++r) {
+    __builtin_amdgcn_s_sleep(32);
+    f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+    ready = __syncthreads_and(f == epoch);
+  }
+  double s = 0.0;
+  if (ready) {
+    double mt[kMeanLoads];
+    load_chunk_sums<D, true>(ksum_part + (int64_t)bh * nch * D + tid % D, nch, tid, mt);
+    s = mean_sum<D>(mt, nch, tid);
+  } else {
+    // the chunk sums of this head, formed here in the same order
+#pragma unroll 1
+    for (int64_t c = 0; c < nch; ++c) {
+      const double cs = chunk_colsum<D, PROD, 2>(src.k, src.stride, src.row0, prod, c, n, ksw, tid);
+      if (tid < D) msum[0][tid] = cs;  // chunk c's column sums
+      __syncthreads();
+      if (c % TPC == tid / D) s += msum[0][tid % D];
+      __syncthreads();
+    }
+  }
+  uint4 w[PASSES];
+  rows_load<D>(src.k, src.stride, tok0, n, tid, w);  // after the mean: fewer registers live
+  head_mean<D>(s, n, msum, mu, blk == 0 ? kmean + (int64_t)bh * D : nullptr, tid);
+  const int64_t co = (int64_t)bh * np * D;
+  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+  if (tok0 + 64 <= n)
+    rows_quant<D, QK, GRAN, PROD, false>(w, src.row0, prod.kw, prod, tok0, n, 1.0f, mu, kc + co, ks + sco, blk_amax,
+                                         tid);
+  else
+    rows_quant<D, QK, GRAN, PROD, true>(w, src.row0, prod.kw, prod, tok0, n, 1.0f, mu, kc + co, ks + sco, blk_amax,
+                                        tid);
+}
+
+// Quantization launch form: one kernel unless the stream is capturing
+// (default), or forced by SAGE_QUANT_PATH: "two" (two kernels), "fallback"
+// (one kernel whose K workgroups form the chunk sums themselves; for tests).
+enum { kQuantAuto = 0, kQuantTwoKernels = 1, kQuantOneFallback = 2 };
+int quant_path() {
+  const char* e = std::getenv("SAGE_QUANT_PATH");
+  if (e == nullptr) return kQuantAuto;
+  if (std::strcmp(e, "two") == 0) return kQuantTwoKernels;
+  if (std::strcmp(e, "fallback") == 0) return kQuantOneFallback;
+  return kQuantAuto;
 }
 
 // Arguments of one quantization call.
@@ -685,20 +1004,48 @@ struct QuantCall {
   float* vs;
   uint16_t* kmean;
   ProdArgs prod;
+  int path;  // kQuantAuto, kQuantTwoKernels, kQuantOneFallback
 };
+
+// A 64-bit value never passed to an earlier launch of this process: a clock
+// reading at first use (distinct across processes) plus a call counter.
+constexpr int64_t kLagUnits = 2048;  // Q and V workgroups dispatched ahead of the first K workgroup
+
+uint64_t next_epoch() {
+  static std::atomic<uint64_t> counter{0};
+  static const uint64_t base =
+      (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count() * 0x9E3779B97F4A7C15ull;
+  return base + counter.fetch_add(1, std::memory_order_relaxed) * 2 + 1;
+}
 
 template <int D, int QK, int PV, int GRAN, bool SMOOTH, bool PROD>
 hipError_t launch_quantize_t(const QuantCall& a, hipStream_t st) {
   const int64_t np = padded_len(a.n);
-  const int nblk = (int)(np / 64);
-  if (SMOOTH) {
-    const int64_t nch = k_sum_chunks(a.n);
-    const dim3 g = PROD ? dim3((unsigned)(nch * a.bh)) : dim3((unsigned)nch, (unsigned)a.bh);
-    hipLaunchKernelGGL((k_colsum_kernel<D, PROD>), g, dim3(256), 0, st, a.k, a.n, a.ws, a.prod);
+  const int64_t nblk = np / 64;
+  if constexpr (SMOOTH) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const hipError_t ce = hipStreamIsCapturing(st, &cap);
+    if (ce != hipSuccess) return ce;
+    if (a.path != kQuantTwoKernels && cap == hipStreamCaptureStatusNone) {
+      const int64_t nch = k_sum_chunks(a.n, D);
+      uint64_t* flags = reinterpret_cast<uint64_t*>(a.ws + a.bh * nch * D);
+      const int64_t grid = nch * a.bh + 3 * nblk * a.bh;
+      hipLaunchKernelGGL((quantize_one_kernel<D, QK, PV, GRAN, PROD>), dim3((unsigned)grid), dim3(256), 0, st, a.q,
+                         a.k, a.v, a.bh, a.n, np, a.fold, a.ws, flags, next_epoch(),
+                         a.path == kQuantOneFallback ? 0 : 4096, min(nblk, (kLagUnits + 2 * a.bh - 1) / (2 * a.bh)), a.qc, a.qs, a.kc, a.ks, a.vout, a.vs, a.kmean,
+                         a.prod);
+      return hipGetLastError();
+    }
   }
-  const dim3 grid = PROD ? dim3((unsigned)((int64_t)nblk * a.bh)) : dim3((unsigned)nblk, (unsigned)a.bh);
-  hipLaunchKernelGGL((quantize_kernel<D, QK, PV, GRAN, SMOOTH, PROD>), grid, dim3(256), 0, st, a.q, a.k, a.v, a.n, np, a.fold, a.ws, a.qc, a.qs, a.kc, a.ks, a.vout, a.vs,
-                     a.kmean, a.prod);
+  constexpr int ROLES = SMOOTH ? 2 : 3;
+  const int64_t nsum = SMOOTH ? k_sum_chunks(a.n, D) * a.bh : 0;
+  hipLaunchKernelGGL((quantize_qv_kernel<D, QK, PV, GRAN, SMOOTH, PROD>), dim3((unsigned)(nsum + ROLES * nblk * a.bh)),
+                     dim3(256), 0, st, a.q, a.k, a.v, a.bh, a.n, np, a.fold, a.ws, a.qc, a.qs, a.kc, a.ks, a.vout,
+                     a.vs, a.prod);
+  if (SMOOTH) {
+    hipLaunchKernelGGL((quantize_k_kernel<D, QK, GRAN, PROD>), dim3((unsigned)(nblk / 2 * a.bh)), dim3(256), 0, st,
+                       a.k, a.bh, a.n, np, a.ws, a.kc, a.ks, a.kmean, a.prod);
+  }
   return hipGetLastError();
 }
 
@@ -726,7 +1073,7 @@ hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t
                            const uint16_t* v, int64_t bh, int64_t n, int64_t d, float fold, double* ws,
                            uint8_t* qc, float* qs, uint8_t* kc, float* ks, uint8_t* vout, float* vs,
                            uint16_t* kmean, const ProdArgs& prod, hipStream_t st) {
-  const QuantCall a{q, k, v, bh, n, fold, ws, qc, qs, kc, ks, vout, vs, kmean, prod};
+  const QuantCall a{q, k, v, bh, n, fold, ws, qc, qs, kc, ks, vout, vs, kmean, prod, quant_path()};
   if (d == 128) return launch_quantize_d<128>(qk, pv, gran, smooth, a, st);
   if (d == 64) return launch_quantize_d<64>(qk, pv, gran, smooth, a, st);
   return hipErrorInvalidValue;
@@ -756,9 +1103,17 @@ hipError_t launch_qkv_postprocess_bwd(const ProdArgs& prod, int64_t bh, int64_t 
   return hipGetLastError();
 }
 
-// fp64 column sums of K per head and 256-token chunk, [bh][ceil(n/256)][d].
+// Workgroups of the largest quantization launch: the column-sum chunks plus
+// three roles per 64-token block, for every head.
+int64_t quant_grid_units(int64_t bh, int64_t n, int64_t d) {
+  return (k_sum_chunks(n, d) + 3 * (padded_len(n) / 64)) * bh;
+}
+
+// fp64 column sums of K per head and chunk, [bh][nch][d], then the chunks'
+// flags of the one-kernel form, uint64 [bh][nch].
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d) {
-  return (size_t)(bh * k_sum_chunks(n) * d) * sizeof(double);
+  const int64_t nch = k_sum_chunks(n, d);
+  return (size_t)(bh * nch * d) * sizeof(double) + (size_t)(bh * nch) * sizeof(uint64_t);
 }
 
 }  // namespace sage

@@ -51,10 +51,15 @@ def test_sizes_and_padding():
     from futudiffu_amd import _lib
     lib = _lib.load()
     assert [lib.sage_padded_len(n) for n in (1, 128, 129, 4416)] == [128, 128, 256, 4480]
-    # fp64 K column sums per head and 256-token chunk
-    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 18 * 128 * 8
-    assert lib.sage_quant_workspace_bytes(2, 256, 64) == 2 * 1 * 64 * 8
-    assert lib.sage_quant_workspace_bytes(1, 257, 64) == 2 * 64 * 8
+    # fp64 K column sums per head and chunk, then an 8-byte flag per chunk;
+    # chunks of 256 tokens, widened by multiples of 256 so that a head has at
+    # most 12 * (256 / D) of them
+    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 18 * (128 + 1) * 8
+    assert lib.sage_quant_workspace_bytes(2, 256, 64) == 2 * 1 * (64 + 1) * 8
+    assert lib.sage_quant_workspace_bytes(1, 257, 64) == 2 * (64 + 1) * 8
+    # 20000 tokens: 79 pieces of 256 -> 1024-token chunks (20) at D=128, 512-token (40) at D=64
+    assert lib.sage_quant_workspace_bytes(1, 20000, 128) == 20 * (128 + 1) * 8
+    assert lib.sage_quant_workspace_bytes(1, 20000, 64) == 40 * (64 + 1) * 8
     # per-batch summaries of every 64-key tile and 32- and 128-row query block,
     # then (256-byte aligned) fp32 slots of 128 x D + 512 floats for the pieces
     # of the split tail: 26 items x 4 pieces (the cap) at the 1x30x4416x128
