@@ -56,11 +56,17 @@ constexpr int64_t kPartFloats = 128 * D + 2 * 256;
 // tiles of pipeline start).  The cap of 4 is measured: at 1050 items of 69
 // tiles, 4 pieces beat 8 (257.6 vs 260.0 us) and 2 (271.7 us), since the
 // partials' traffic and merge grow with the piece count and the pieces run
-// beside the second round's last items.  Launches of less than one round are
-// not cut: there every item
-// would be cut, and the partials' traffic and the merge then cost more than
-// the balance gains (measured at 300 items of 20 tiles: 50.6 us uncut,
-// 57.9 / 59.8 / 61.9 us in 2 / 3 / 4 pieces).
+// beside the second round's last items.
+//
+// Launches of less than one round: an item alone on a CU runs about 1.4x
+// faster than one of two sharing it (its waves have the SIMDs' issue slots to
+// themselves), so when up to 128 items spill past one per CU, the first 256
+// stay whole and the spilled items are cut in two key halves that share the
+// CUs with them (measured at 20 tiles, kernel + merge: 260 items 43.5 ->
+// 34.8 us, 300 items 41.6 -> 36.9, 350 items 41.5 -> 39.1; 400 items lose,
+// 42.1 -> 55.7).  Cutting every item costs more than it balances (300 items:
+// 54.3 / 57.7 / 59.6 us in 2 / 3 / 4 pieces), as do more pieces of the
+// spilled items (300 items: 37.5 / 37.9 us in 3 / 4).
 struct TailSplit {
   int64_t whole;
   int parts;
@@ -68,6 +74,11 @@ struct TailSplit {
 
 inline TailSplit tail_split(int64_t n_items, int64_t nt) {
   TailSplit t{n_items, 1};
+  constexpr int64_t kCUs = kResidentWGs / 2;
+  if (n_items > kCUs && n_items < kResidentWGs) {
+    if (n_items - kCUs <= 128 && nt >= 2) t = TailSplit{kCUs, 2};
+    return t;
+  }
   const int64_t rest = n_items >= kResidentWGs ? n_items % kResidentWGs : 0;
   if (rest == 0) return t;
   int64_t best = (rest + kResidentWGs - 1) / kResidentWGs * (nt + 2);

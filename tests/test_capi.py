@@ -63,10 +63,12 @@ def test_sizes_and_padding():
     # per-batch summaries of every 64-key tile and 32- and 128-row query block,
     # then (256-byte aligned) fp32 slots of 128 x D + 512 floats for the pieces
     # of the split tail: 26 items x 4 pieces (the cap) at the 1x30x4416x128
-    # headline shape (1050 items = 2 rounds of 512 + 26), none below one round
-    # of 512 items
+    # headline shape (1050 items = 2 rounds of 512 + 26); below one round,
+    # the items past one per CU (256) in two halves when at most 128 of them:
+    # 300 items at 1x30x1280 -> 44 x 2, 400 items (1x40x1280) uncut
     for b, h, n, d, pieces in ((2, 3, 200, 128, 0), (1, 30, 4416, 128, 26 * 4), (1, 1, 1, 64, 0),
-                               (1, 30, 1280, 128, 0), (2, 30, 4416, 128, 52 * 4)):
+                               (1, 30, 1280, 128, 44 * 2), (1, 40, 1280, 128, 0), (1, 26, 1280, 128, 4 * 2),
+                               (2, 30, 4416, 128, 52 * 4)):
         np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
         doc = (b * (nt + np_ // 32 + np_ // 128) * 16 + 255) // 256 * 256
         assert lib.sage_attn_workspace_bytes(b, h, n, d) == doc + pieces * (128 * d + 512) * 4
@@ -94,6 +96,7 @@ def _quant_call(lib, **over):
     (dict(ws=176, wsb=8), 3, "workspace"),
     (dict(ws=184, wsb=1 << 20), 2, "workspace must be 16-byte aligned"),
     (dict(bh=70000), 1, "grid"),
+    (dict(bh=65535, n=1 << 24), 1, "beyond one launch"),
 ])
 @fake_addresses
 def test_quantize_rejects_bad_arguments(over, status, msg):
@@ -150,6 +153,7 @@ def _prod_args(**over):
     (dict(fr=None), 1, "null"),
     (dict(qw=40), 2, "aligned"),
     (dict(eps=-1.0), 1, "norm_eps"),
+    (dict(h=30000), 1, "too wide"),
 ])
 @fake_addresses
 def test_producer_entries_reject_bad_arguments(over, status, msg):
