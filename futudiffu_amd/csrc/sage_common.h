@@ -29,13 +29,9 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (the rounding torch uses for bf16 results).
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> bf16, round to nearest even (the rounding torch uses for bf16
+// results): gfx950's v_cvt_pk_bf16_f32.  NaN stays NaN (quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // Two fp32 -> two OCP e4m3fn codes (RNE, saturating) packed into 16 bits.
 __device__ __forceinline__ uint32_t pack_fp8x2(float a, float b) {
