@@ -741,6 +741,8 @@ def main():
             "unit": "GB/s",
             "frac": round(q_gbs / PEAK_HBM_GBS, 4),
             "algorithmic_bytes": qbytes,
+            "traffic": profiled_traffic(workload, "quantize_one_kernel"),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0; K is read twice)",
             "avg_ms": round(q_avg, 5),
             # the same traffic as a plain 2:1 stream, measured here after the timed steps
             "stream_2to1_GBs": round(q_stream, 1),
