@@ -130,10 +130,7 @@ template <int D, int PV>
 struct Smem {
   static constexpr int kStages = PV == kPV_FP8 ? 4 : 3;
   static constexpr int offX = kStages * Stage<D, PV>::bytes;
-  // per-wave key bias rows (0 or -inf per key of a tile) and a row of zeros,
-  // for document-id visibility in the pipelined fp8 loop
-  static constexpr int offBias = offX + 4 * 32 * 4;
-  static constexpr int bytes = offBias + 5 * 64 * 4;
+  static constexpr int bytes = offX + 4 * 32 * 4;
   static_assert(4 * 32 * D * 2 <= offX, "epilogue staging must fit in the stage ring");
 };
 
@@ -294,34 +291,6 @@ __device__ __forceinline__ void half_scores(const uint8_t* sb, const typename SA
   }
 }
 
-// half_scores with the key visibility as an additive bias per key (0 or
-// -inf): u = acc * kd + bias, one fused operation per score.  bias points at
-// 64 floats in LDS, laid out like the stage's per-key K scales.
-template <int D, int QK, int PV, int GRAN>
-__device__ __forceinline__ void half_scores_bias(const uint8_t* sb, const typename SAccT<QK>::type& s, int b, int h,
-                                                 float kd_blk, int kvalid, const f32x4* bias, float (&u)[16]) {
-  using St = Stage<D, PV>;
-  const f32x4* kdl = reinterpret_cast<const f32x4*>(sb + St::offKd);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f32x4 kd4;
-    if constexpr (GRAN == kGRAN_TOKEN)
-      kd4 = kdl[8 * b + 2 * j + h];
-    else
-      kd4 = f32x4{kd_blk, kd_blk, kd_blk, kd_blk};
-    const f32x4 bi4 = bias[8 * b + 2 * j + h];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) u[4 * j + i] = fmaf((float)s[4 * j + i], kd4[i], bi4[i]);
-  }
-  if (kvalid < 64) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (32 * b + 8 * j + 4 * h + i >= kvalid) u[4 * j + i] = -INFINITY;
-  }
-}
-
 // Row max of the tile's 32 scores per lane (max3 tree, then across the two
 // lane halves) in log2 units, and the lazy frame move: the reference point
 // m_ref moves to the block max bm when bm exceeds it by more than kTau, and
@@ -431,18 +400,13 @@ template <int D, int QK, int PV, int GRAN, int MASK, bool MASKED>
 __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_next, const i32x4* qf, int lane,
                                           typename SAccT<QK>::type& s0, typename SAccT<QK>::type& s1, f32x16* o,
                                           float& m_ref, float& l_acc, float wt, float* xrow, int dq, float kd_blk,
-                                          int kvalid, const f32x4* key_bias = nullptr) {
+                                          int kvalid) {
   using St = Stage<D, PV>;
   constexpr int NC = D / 32;
   const int h = lane >> 5, r = lane & 31;
   float u[2][16];
-  if (key_bias != nullptr) {
-    half_scores_bias<D, QK, PV, GRAN>(sb, s0, 0, h, kd_blk, kvalid, key_bias, u[0]);
-    half_scores_bias<D, QK, PV, GRAN>(sb, s1, 1, h, kd_blk, kvalid, key_bias, u[1]);
-  } else {
-    half_scores<D, QK, PV, GRAN, MASKED>(sb, s0, 0, h, kd_blk, kvalid, true, dq, u[0]);
-    half_scores<D, QK, PV, GRAN, MASKED>(sb, s1, 1, h, kd_blk, kvalid, true, dq, u[1]);
-  }
+  half_scores<D, QK, PV, GRAN, MASKED>(sb, s0, 0, h, kd_blk, kvalid, true, dq, u[0]);
+  half_scores<D, QK, PV, GRAN, MASKED>(sb, s1, 1, h, kd_blk, kvalid, true, dq, u[1]);
   qk_both<D, QK>(sb_next, qf, lane, s0, s1);
   if constexpr (PV == kPV_FP8) {
     i32x8 pa;
@@ -493,12 +457,8 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
 // Ends with a workgroup barrier, after which the stage ring may be reused.
 // DUMP (int8 QK only) also stores every S^T accumulator pair this loop
 // consumes into p.s_dump, at the point where it is consumed.
-// DM splits fp8 P.V launches with document ids in two: 1 runs the items
-// that the pipelined loop can take (below), 2 the others on the general loop;
-// each returns false, having computed and stored nothing, for the items of
-// the other.  Every other launch has DM 0.
-template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false, int DM = 0>
-__device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, int bh, int qt, int t_begin,
+template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false>
+__device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, int bh, int qt, int t_begin,
                                            int t_end, f32x16* o, float& m_ref, float& l_acc) {
   using St = Stage<D, PV>;
   using SM = Smem<D, PV>;
@@ -626,48 +586,6 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
 
   constexpr bool kFast = PV == kPV_FP8;
   constexpr bool DOC = (MASK & 2) != 0;
-  static_assert(!(kFast && DOC) || DM != 0, "fp8 P.V with document ids runs as two launches");
-  // Document ids on the pipelined fp8 loop: a tile's visibility must be the
-  // same for every row of a wave that does not see all of it, so that it is
-  // one additive bias per key (0 or -inf).  That holds when the wave's valid
-  // rows share one document (padded rows see every valid key, which is then
-  // that document's keys only if the tile holds no other), or when all its
-  // rows are padding.  Every wave evaluates the same test over all tiles of
-  // the item, and finds the last tile that some wave does not see whole: the
-  // tiles up to it take the loop body with the per-key bias, the rest the
-  // plain body.
-  int prefix_end = t_begin;
-  if constexpr (kFast && DOC) {
-    int4 qs[4];
-#pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4) qs[w4] = load_uniform(p.q_sum, (int64_t)bidx * (p.np / 32) + qt * 4 + w4);
-    bool ok = true;
-    int last = t_begin - 1;
-    for (int tt = t_begin + lane; tt < t_end; tt += 64) {
-      const int4 ks = p.kv_sum[(int64_t)bidx * p.nt + tt];
-      if (classify(qsum128, ks) == 0) continue;  // no row of the item sees it: not scheduled
-#pragma unroll
-      for (int w4 = 0; w4 < 4; ++w4) {
-        const int4 qw = qs[w4];
-        if (qw.z + qw.w == 0) continue;  // wave past N
-        const int c = classify(qw, ks);
-        if (c != 1) last = tt;
-        if (c != 2) continue;
-        const bool all_pad = qw.z == 0;
-        const bool one_doc = qw.z > 0 && qw.x == qw.y;
-        const bool keys_one = ks.z == 0 || (ks.x == ks.y && ks.x == qw.x);
-        if (!(all_pad || (one_doc && (qw.w == 0 || keys_one)))) ok = false;
-      }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) last = max(last, __shfl_xor(last, off));
-    prefix_end = last + 1;
-    const bool eligible = !__any(!ok);
-    if (DM == 1 && !eligible) return false;
-    if (DM == 2 && eligible) return false;
-    if (DM == 1 && wave == 0) reinterpret_cast<float*>(smem + SM::offBias + 4 * 256)[lane] = 0.0f;
-  }
-
   // ---- prologue: tiles 0 and 1 of the schedule in stages 0 and 1 --------------
   int t = next_active(t_begin);
   int t1 = t < t_end ? next_active(t + 1) : t_end;
@@ -680,6 +598,13 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     load_tile(t1, smem + St::bytes);
     store_doc(smem + St::bytes);
   }
+  // Document ids with fp8 P.V: the pipelined loop computes every scheduled
+  // tile in every live wave with no visibility test, which holds for a tile
+  // that every live wave sees whole.  The tiles before prefix_end (one past
+  // the last that some live wave does not see whole, from doc_prefix_kernel)
+  // go through the general tile body with its per-element visibility test.
+  int prefix_end = t_begin;
+  if constexpr (kFast && DOC) prefix_end = load_uniform(p.doc_prefix, (int64_t)bidx * nq + qt);
   wait_vmem();
   __syncthreads();
   SAcc s0, s1;  // S^T of the tile about to be consumed
@@ -687,155 +612,11 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     qk_both<D, QK>(smem, qf, lane, s0, s1);
   }
 
+  // one tile of the general loop: tile t2 into a stage no wave reads any more
+  // (the last barrier ended every read of it), tile t through tile_body with
+  // this wave's visibility class, the next tile's S^T, publish, advance
   constexpr int kSt = SM::kStages;
-  if constexpr (kFast && DM != 2) {
-   {
-    // ---- fp8 P.V: every scheduled tile is computed by every live wave, so
-    // the product of tile i-1 is always pending in iteration i.  The first
-    // and the last tile are peeled off the loop, which leaves its body one
-    // straight basic block for the scheduler: the pending P.V in two
-    // chunk-pair halves, each under half of this tile's score conversion,
-    // then the next tile's S^T under this tile's softmax.  With document ids
-    // the schedule holds the tiles some row of the workgroup sees; a wave
-    // whose rows do not all see every key of the tile applies the per-token
-    // visibility in its score conversion (invisible scores are -inf: their
-    // P codes are 0, and a row that sees nothing keeps its frame).
-    constexpr int NP = NC / 2;
-    auto wave_masked = [&](int tt) -> bool {
-      if constexpr (DOC) return classify(qsum, load_uniform(p.kv_sum, (int64_t)bidx * p.nt + tt)) != 1;
-      return false;
-    };
-    // this wave's key bias for a tile it does not fully see (written from the
-    // stage's key document ids), or the row of zeros
-    float* bias_row = reinterpret_cast<float*>(smem + SM::offBias) + 64 * wave;
-    const f32x4* zero_row = reinterpret_cast<const f32x4*>(smem + SM::offBias + 4 * 256);
-    auto key_bias = [&](const uint8_t* sbk, int tt) -> const f32x4* {
-      if (tt >= prefix_end) return zero_row;
-      const int dk = reinterpret_cast<const int*>(sbk + St::offDoc)[lane];
-      const bool vis = qsum.z == 0 ? dk >= 0 : dk == qsum.x;
-      bias_row[lane] = vis ? 0.0f : -INFINITY;
-      // the row passes between lanes: wavefront-scope fences (see rows_of)
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      return reinterpret_cast<const f32x4*>(bias_row);
-    };
-    int stage = 0;
-    auto sp = [&](int s_) { return smem + s_ * St::bytes; };
-    auto next_stage = [&](int s_, int k_) { return (s_ + k_) % kSt; };
-    auto advance = [&]() __attribute__((always_inline)) {
-      stage = next_stage(stage, 1);
-      t = t1;
-      t1 = t2;
-      t2 = t2 < t_end ? next_active(t2 + 1) : t_end;
-    };
-    auto publish = [&]() __attribute__((always_inline)) {
-      if (t2 < t_end) store_doc(sp(next_stage(stage, 2)));
-      wait_vmem();
-      __syncthreads();
-    };
-    if (!wave_live) {
-      // rows past N: the same loads and barriers, nothing computed
-      while (t < t_end) {
-        if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
-        publish();
-        advance();
-      }
-      __syncthreads();
-      return true;
-    }
-    const bool any = t < t_end;
-    i32x8 pa_p = {0, 0, 0, 0, 0, 0, 0, 0};
-    float rsc_p = 0.0f;
-    int stage_p = 0;
-    float u[2][16];
-    if (t < t_end) {  // first tile: nothing pending
-      if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
-      dump(t, s0, s1);
-      const float kdb = kd_block(t);
-      const int kvalid = keys_valid(t);
-      if (DOC && t < prefix_end) {
-        const f32x4* bias = key_bias(sp(stage), t);
-        half_scores_bias<D, QK, PV, GRAN>(sp(stage), s0, 0, h, kdb, kvalid, bias, u[0]);
-        half_scores_bias<D, QK, PV, GRAN>(sp(stage), s1, 1, h, kdb, kvalid, bias, u[1]);
-      } else {
-        half_scores<D, QK, PV, GRAN, false>(sp(stage), s0, 0, h, kdb, kvalid, false, dq, u[0]);
-        half_scores<D, QK, PV, GRAN, false>(sp(stage), s1, 1, h, kdb, kvalid, false, dq, u[1]);
-      }
-      if (t1 < t_end) qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
-      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
-      stage_p = stage;
-      publish();
-      advance();
-    }
-    // one iteration for a whole tile t with a successor; BIAS: the tile may
-    // be one that this wave does not see whole
-    auto iteration = [&](auto bias_tag) __attribute__((always_inline)) {
-      constexpr bool BIAS = decltype(bias_tag)::value;
-      if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
-      const uint8_t* sb = sp(stage);
-      const uint8_t* sbp = sp(stage_p);
-      const float kdb = kd_block(t);
-      const f32x4* bias = BIAS ? key_bias(sb, t) : zero_row;
-      dump(t, s0, s1);
-      auto scores = [&](int b_, float (&u_)[16]) __attribute__((always_inline)) {
-        if constexpr (BIAS)
-          half_scores_bias<D, QK, PV, GRAN>(sb, b_ ? s1 : s0, b_, h, kdb, 64, bias, u_);
-        else
-          half_scores<D, QK, PV, GRAN, false>(sb, b_ ? s1 : s0, b_, h, kdb, 64, false, dq, u_);
-      };
-      f32x16 p0, p1;
-      f32x32 rv;
-      pv_issue<D>(sbp, pa_p, rsc_p, lane, 0, p0, p1, rv);
-      scores(0, u[0]);
-      if constexpr (NP == 1) scores(1, u[1]);
-      pv_accum(o, 0, p0, p1, rv);
-      if constexpr (NP == 2) {
-        pv_issue<D>(sbp, pa_p, rsc_p, lane, 2, p0, p1, rv);
-        scores(1, u[1]);
-        pv_accum(o, 2, p0, p1, rv);
-      }
-      qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
-      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
-      stage_p = stage;
-      publish();
-      advance();
-    };
-    while (t1 < t_end) iteration(std::integral_constant<bool, DOC>{});
-    if (t < t_end) {  // last tile: the pending product, then the tile with its P.V formed at once
-      const uint8_t* sbp = sp(stage_p);
-#pragma unroll
-      for (int c2 = 0; c2 < NC; c2 += 2) {
-        f32x16 p0, p1;
-        f32x32 rv;
-        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
-        pv_accum(o, c2, p0, p1, rv);
-        __builtin_amdgcn_sched_barrier(0);  // one pair's products in flight at a time
-      }
-      const uint8_t* sb = sp(stage);
-      dump(t, s0, s1);
-      tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kd_block(t),
-                                              keys_valid(t), DOC && t < prefix_end ? key_bias(sb, t) : nullptr);
-      publish();
-      advance();
-    } else if (any) {  // the single tile was also the first: its product is pending
-      const uint8_t* sbp = sp(stage_p);
-#pragma unroll
-      for (int c2 = 0; c2 < NC; c2 += 2) {
-        f32x16 p0, p1;
-        f32x32 rv;
-        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
-        pv_accum(o, c2, p0, p1, rv);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    __syncthreads();  // the ring is reused after
-    return true;
-   }
-  }
-  if constexpr (!kFast || DM == 2) {
-  int stage = 0;
-  while (t < t_end) {
+  auto general_step = [&](int& stage) __attribute__((always_inline)) {
     const uint8_t* sb = smem + stage * St::bytes;
     const int stage1 = stage + 1 == kSt ? 0 : stage + 1;
     const int stage2 = stage1 + 1 == kSt ? 0 : stage1 + 1;
@@ -867,9 +648,128 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     t = t1;
     t1 = t2;
     t2 = t2 < t_end ? next_active(t2 + 1) : t_end;
+  };
+  if constexpr (kFast) {
+   {
+    // ---- fp8 P.V: every scheduled tile is computed by every live wave, so
+    // the product of tile i-1 is always pending in iteration i.  The first
+    // and the last tile are peeled off the loop, which leaves its body one
+    // straight basic block for the scheduler: the pending P.V in two
+    // chunk-pair halves, each under half of this tile's score conversion,
+    // then the next tile's S^T under this tile's softmax.  With document ids
+    // the tiles before prefix_end, which some live wave does not see whole,
+    // go through the general body first; every later scheduled tile is seen
+    // whole by every live wave.
+    constexpr int NP = NC / 2;
+    int stage = 0;
+    if constexpr (DOC) {
+      while (t < t_end && t < prefix_end) general_step(stage);
+    }
+    auto sp = [&](int s_) { return smem + s_ * St::bytes; };
+    auto next_stage = [&](int s_, int k_) { return (s_ + k_) % kSt; };
+    auto advance = [&]() __attribute__((always_inline)) {
+      stage = next_stage(stage, 1);
+      t = t1;
+      t1 = t2;
+      t2 = t2 < t_end ? next_active(t2 + 1) : t_end;
+    };
+    auto publish = [&]() __attribute__((always_inline)) {
+      if (t2 < t_end) store_doc(sp(next_stage(stage, 2)));
+      wait_vmem();
+      __syncthreads();
+    };
+    if (!wave_live) {
+      // rows past N: the same loads and barriers, nothing computed
+      while (t < t_end) {
+        if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+        publish();
+        advance();
+      }
+      __syncthreads();
+      return;
+    }
+    const bool any = t < t_end;
+    i32x8 pa_p = {0, 0, 0, 0, 0, 0, 0, 0};
+    float rsc_p = 0.0f;
+    int stage_p = 0;
+    float u[2][16];
+    if (t < t_end) {  // first tile: nothing pending
+      if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+      dump(t, s0, s1);
+      const float kdb = kd_block(t);
+      const int kvalid = keys_valid(t);
+      half_scores<D, QK, PV, GRAN, false>(sp(stage), s0, 0, h, kdb, kvalid, false, dq, u[0]);
+      half_scores<D, QK, PV, GRAN, false>(sp(stage), s1, 1, h, kdb, kvalid, false, dq, u[1]);
+      if (t1 < t_end) qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
+      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
+      stage_p = stage;
+      publish();
+      advance();
+    }
+    // one iteration for a whole tile t with a successor
+    auto iteration = [&]() __attribute__((always_inline)) {
+      if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+      const uint8_t* sb = sp(stage);
+      const uint8_t* sbp = sp(stage_p);
+      const float kdb = kd_block(t);
+      dump(t, s0, s1);
+      auto scores = [&](int b_, float (&u_)[16]) __attribute__((always_inline)) {
+        half_scores<D, QK, PV, GRAN, false>(sb, b_ ? s1 : s0, b_, h, kdb, 64, false, dq, u_);
+      };
+      f32x16 p0, p1;
+      f32x32 rv;
+      pv_issue<D>(sbp, pa_p, rsc_p, lane, 0, p0, p1, rv);
+      scores(0, u[0]);
+      if constexpr (NP == 1) scores(1, u[1]);
+      pv_accum(o, 0, p0, p1, rv);
+      if constexpr (NP == 2) {
+        pv_issue<D>(sbp, pa_p, rsc_p, lane, 2, p0, p1, rv);
+        scores(1, u[1]);
+        pv_accum(o, 2, p0, p1, rv);
+      }
+      qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
+      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
+      stage_p = stage;
+      publish();
+      advance();
+    };
+    while (t1 < t_end) iteration();
+    if (t < t_end) {  // last tile: the pending product, then the tile with its P.V formed at once
+      const uint8_t* sbp = sp(stage_p);
+#pragma unroll
+      for (int c2 = 0; c2 < NC; c2 += 2) {
+        f32x16 p0, p1;
+        f32x32 rv;
+        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
+        pv_accum(o, c2, p0, p1, rv);
+        __builtin_amdgcn_sched_barrier(0);  // one pair's products in flight at a time
+      }
+      const uint8_t* sb = sp(stage);
+      dump(t, s0, s1);
+      tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kd_block(t),
+                                              keys_valid(t));
+      publish();
+      advance();
+    } else if (any) {  // the single tile was also the first: its product is pending
+      const uint8_t* sbp = sp(stage_p);
+#pragma unroll
+      for (int c2 = 0; c2 < NC; c2 += 2) {
+        f32x16 p0, p1;
+        f32x32 rv;
+        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
+        pv_accum(o, c2, p0, p1, rv);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __syncthreads();  // the ring is reused after
+    return;
+   }
   }
+  if constexpr (!kFast) {
+    int stage = 0;
+    while (t < t_end) general_step(stage);
   }
-  return true;
+  return;
 }
 
 constexpr int kRawBufferWord3 = 0x00020000;  // word 3 of a raw (untyped) buffer resource, gfx9 family
@@ -943,7 +843,7 @@ __device__ __forceinline__ void store_partial(float* slot, const f32x16* o, floa
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_acc), rs, tid * 4, (128 * D + 256) * 4, 0);
 }
 
-template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false, int DM = 0>
+template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   using SM = Smem<D, PV>;
   constexpr int NC = D / 32;
@@ -980,8 +880,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   } else {
     item_of(blockIdx.x, (int)gridDim.x, p.bh, nq, p.light_last, bh, qt);
   }
-  if (item_tiles<D, QK, PV, GRAN, MASK, DUMP, DM>(p, smem, bh, qt, 0, p.nt, o, m_ref, l_acc))
-    store_rows_final<D, PV>(p, smem, bh, qt, o, m_ref, l_acc);
+  item_tiles<D, QK, PV, GRAN, MASK, DUMP>(p, smem, bh, qt, 0, p.nt, o, m_ref, l_acc);
+  store_rows_final<D, PV>(p, smem, bh, qt, o, m_ref, l_acc);
 }
 
 // Merges the pieces of the split items.  Block (split item, 32-row block w,
@@ -1072,24 +972,8 @@ hipError_t launch_attn_g(int mask, const AttnParams& p, hipStream_t st) {
   } else switch (mask) {
     case 0: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 0>), grid, dim3(256), 0, st, p); break;
     case 1: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 1>), grid, dim3(256), 0, st, p); break;
-    case 2:
-    case 3:
-      // document ids: the items the pipelined fp8 loop can take, then the
-      // others on the general loop (bf16 P.V has only the general loop)
-      if constexpr (PV == kPV_FP8) {
-        if (mask == 2) {
-          hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 2, false, 1>), grid, dim3(256), 0, st, p);
-          hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 2, false, 2>), grid, dim3(256), 0, st, p);
-        } else {
-          hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 3, false, 1>), grid, dim3(256), 0, st, p);
-          hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 3, false, 2>), grid, dim3(256), 0, st, p);
-        }
-      } else if (mask == 2) {
-        hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 2>), grid, dim3(256), 0, st, p);
-      } else {
-        hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 3>), grid, dim3(256), 0, st, p);
-      }
-      break;
+    case 2: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 2>), grid, dim3(256), 0, st, p); break;
+    case 3: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 3>), grid, dim3(256), 0, st, p); break;
   }
   if (n_split > 0)
     hipLaunchKernelGGL(merge_split_kernel<D>, dim3((unsigned)n_split, 4, 4), dim3(256), 0, st, p);
@@ -1106,6 +990,49 @@ hipError_t launch_attn_d(int qk, int pv, int gran, int mask, const AttnParams& p
   return hipErrorInvalidValue;
 }
 
+// One wave per (batch, 128-row query tile): lanes scan the key tiles, the
+// scheduled ones (some row of the query tile sees a key) that some live
+// 32-row wave of the tile does not see whole (classify != 1); the result is
+// one past the last of them.  The pipelined fp8 loop of the attention kernel
+// takes the tiles from there on; the tiles before go through the general
+// tile body with its per-element visibility test.
+__global__ void __launch_bounds__(256) doc_prefix_kernel(const int4* __restrict__ kv_sum,
+                                                         const int4* __restrict__ q_sum,
+                                                         const int4* __restrict__ q_sum128, int nb, int nq, int nt,
+                                                         int32_t* __restrict__ prefix) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // wave-uniform
+  if (item >= (int64_t)nb * nq) return;
+  const int b = (int)(item / nq), qt = (int)(item % nq);
+  const int4 q128 = q_sum128[(int64_t)b * nq + qt];
+  int4 qs[4];
+#pragma unroll
+  for (int w4 = 0; w4 < 4; ++w4) qs[w4] = q_sum[(int64_t)b * nq * 4 + qt * 4 + w4];
+  int last = -1;
+  for (int t = lane; t < nt; t += 64) {
+    const int4 ks = kv_sum[(int64_t)b * nt + t];
+    if (classify(q128, ks) == 0) continue;  // not scheduled
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4) {
+      if (qs[w4].z + qs[w4].w == 0) continue;  // wave past N
+      if (classify(qs[w4], ks) != 1) last = t;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) last = max(last, __shfl_xor(last, off));
+  if (lane == 0) prefix[item] = last + 1;
+}
+
+hipError_t launch_doc_prefix(const int4* kv_sum, const int4* q_sum, const int4* q_sum128, int64_t n, int nb,
+                             int32_t* prefix, hipStream_t st) {
+  const int nq = (int)(padded_len(n) / 128);
+  const int nt = (int)((n + 63) / 64);
+  const int64_t waves = (int64_t)nb * nq;
+  hipLaunchKernelGGL(doc_prefix_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, kv_sum, q_sum, q_sum128,
+                     nb, nq, nt, prefix);
+  return hipGetLastError();
+}
+
 hipError_t launch_doc_summaries(const int32_t* doc, int64_t n, int nb, int4* kv_sum, int4* q_sum, int4* q_sum128,
                                 hipStream_t st) {
   const int64_t np = padded_len(n);
@@ -1120,9 +1047,13 @@ hipError_t launch_doc_summaries(const int32_t* doc, int64_t n, int nb, int4* kv_
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb,
                        hipStream_t st) {
   if (mask & 2) {
-    const hipError_t e = launch_doc_summaries(p.doc, p.n, nb, const_cast<int4*>(p.kv_sum),
-                                              const_cast<int4*>(p.q_sum), const_cast<int4*>(p.q_sum128), st);
+    hipError_t e = launch_doc_summaries(p.doc, p.n, nb, const_cast<int4*>(p.kv_sum), const_cast<int4*>(p.q_sum),
+                                        const_cast<int4*>(p.q_sum128), st);
     if (e != hipSuccess) return e;
+    if (pv == kPV_FP8) {
+      e = launch_doc_prefix(p.kv_sum, p.q_sum, p.q_sum128, p.n, nb, const_cast<int32_t*>(p.doc_prefix), st);
+      if (e != hipSuccess) return e;
+    }
   }
   if (d == 128) return launch_attn_d<128>(qk, pv, gran, mask, p, st);
   if (d == 64) return launch_attn_d<64>(qk, pv, gran, mask, p, st);
@@ -1136,7 +1067,9 @@ AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d) {
   AttnWorkspace w;
   w.split = tail_split(items, nt);
   w.doc_off = 0;
-  w.part_off = ((size_t)(b * (nt + np / 32 + np / 128)) * sizeof(int4) + 255) & ~(size_t)255;
+  // summaries (int4), then the fp8 loop's per-query-tile prefixes (int32)
+  w.part_off = ((size_t)(b * (nt + np / 32 + np / 128)) * sizeof(int4) + (size_t)(b * (np / 128)) * sizeof(int32_t) +
+                255) & ~(size_t)255;
   const int64_t pieces = w.split.parts > 1 ? (items - w.split.whole) * w.split.parts : 0;
   w.bytes = w.part_off + (size_t)pieces * (size_t)(128 * d + 512) * sizeof(float);
   return w;

@@ -118,6 +118,10 @@ __device__ __forceinline__ int4 load_uniform(const int4* base, int64_t i) {
   const ConstPtr q = (ConstPtr)(base + i);
   return make_int4(q[0], q[1], q[2], q[3]);
 }
+__device__ __forceinline__ int32_t load_uniform(const int32_t* base, int64_t i) {
+  typedef const __attribute__((address_space(4))) int32_t* ConstPtr;
+  return *(ConstPtr)(base + i);
+}
 __device__ __forceinline__ float load_uniform(const float* base, int64_t i) {
   typedef const __attribute__((address_space(4))) float* ConstPtr;
   return *(ConstPtr)(base + i);
