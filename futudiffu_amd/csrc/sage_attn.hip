@@ -10,9 +10,10 @@
 // query rows.  Keys stream in 64-key tiles (the reference KV tile, which is
 // also the V-scale block) through a ring of LDS stages filled by direct
 // global -> LDS loads: tile i+2 is issued while tile i is consumed and tile
-// i+1 already feeds the next S^T; one barrier per tile.  With fp8 P.V (int8
-// QK, per-token scales) the product of tile i-1 is formed in iteration i, its
-// MFMAs under tile i's score conversion (four stages).
+// i+1 already feeds the next S^T; one barrier per tile.  Without document
+// ids (and with them for fp8 P.V) the loop is software-pipelined: the P.V of
+// tile i-1 is formed in iteration i, its MFMAs under tile i's score
+// conversion and softmax.
 //
 // Per wave and tile:
 //   S^T[key][query] = K . Q^T with v_mfma_i32_32x32x32_i8 (int8) or
@@ -122,10 +123,13 @@ struct Stage {
 };
 
 // Workgroup LDS: a ring of stages, then a 32-float row exchange per wave.  With
-// bf16 P.V three stages: tile i is consumed while tile i+1 feeds the next
-// QK^T and tile i+2 is being written.  With fp8 P.V the product of tile i-1 is
-// formed while tile i is consumed, so its V stays resident one tile longer:
-// four stages.  The bf16 output staging of the epilogue reuses the ring.
+// fp8 P.V four stages: the product of tile i-1 is formed while tile i is
+// consumed, tile i+1 feeds the next QK^T and tile i+2 is being written.  With
+// bf16 P.V (a stage of 24.5 KB at D = 128) three stages: in the pipelined
+// loop a tile's K part is loaded two tiles ahead and the rest one tile ahead,
+// so K of tile i+2 shares a stage with V of tile i-1; in the general loop
+// tile i is consumed while tile i+1 feeds the next QK^T and tile i+2 is being
+// written.  The bf16 output staging of the epilogue reuses the ring.
 template <int D, int PV>
 struct Smem {
   static constexpr int kStages = PV == kPV_FP8 ? 4 : 3;
@@ -296,10 +300,11 @@ __device__ __forceinline__ void half_scores(const uint8_t* sb, const typename SA
 // m_ref moves to the block max bm when bm exceeds it by more than kTau, and
 // O and l are rescaled then (branch-free values, the O rescale only when some
 // row of the wave moves).  Returns bm (-inf for a row that sees no key).
-template <int D>
-__device__ __forceinline__ float row_max_move(float (&u)[2][16], float wt, float& m_ref, float& l_acc, f32x16* o,
-                                              float* xrow, int h, int r) {
-  constexpr int NC = D / 32;
+// row_max_frame decides the move and rescales l; it sets any_move when some
+// row of the wave moved, and the caller rescales O by alpha (frame_move_o),
+// at once (row_max_move) or before the next product is added to O.
+__device__ __forceinline__ float row_max_frame(float (&u)[2][16], float wt, float& m_ref, float& l_acc, float& alpha,
+                                               bool& any_move) {
   constexpr float kTau = 8.0f;
   float mx;
   {
@@ -321,17 +326,32 @@ __device__ __forceinline__ float row_max_move(float (&u)[2][16], float wt, float
   const float bm = mx * wt;  // -inf if nothing visible in this row
   const bool row_live = bm > -INFINITY;
   const bool move = row_live && !(bm <= m_ref + kTau);
-  const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - bm) : 1.0f;  // 0 when m_ref = -inf
+  alpha = move ? __builtin_amdgcn_exp2f(m_ref - bm) : 1.0f;  // 0 when m_ref = -inf
   m_ref = move ? bm : m_ref;
   l_acc *= alpha;
-  if (__any(move)) {
-    float arow[16];
-    rows_of(xrow, alpha, h, r, arow);
+  any_move = __any(move);
+  return bm;
+}
+
+// O *= alpha of its row (the frame move of row_max_frame).
+template <int D>
+__device__ __forceinline__ void frame_move_o(f32x16* o, float* xrow, float alpha, int h, int r) {
+  constexpr int NC = D / 32;
+  float arow[16];
+  rows_of(xrow, alpha, h, r, arow);
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[c][e] *= arow[e];
-  }
+    for (int e = 0; e < 16; ++e) o[c][e] *= arow[e];
+}
+
+template <int D>
+__device__ __forceinline__ float row_max_move(float (&u)[2][16], float wt, float& m_ref, float& l_acc, f32x16* o,
+                                              float* xrow, int h, int r) {
+  float alpha;
+  bool any_move;
+  const float bm = row_max_frame(u, wt, m_ref, l_acc, alpha, any_move);
+  if (any_move) frame_move_o<D>(o, xrow, alpha, h, r);
   return bm;
 }
 
@@ -390,6 +410,45 @@ __device__ __forceinline__ void pv_accum(f32x16* o, int c2, const f32x16& p0, co
   for (int e = 0; e < 16; ++e) o[c2 + 1][e] = fmaf(p1[e], rv[16 + e], o[c2 + 1][e]);
 }
 
+// bf16 P of the tile: 2^(s - m_ref) <= 2^kTau after the frame decision, row
+// sums into l.  O is not touched: the caller applies the move (alpha, when
+// the result is true) to O before it adds this tile's product.
+__device__ __forceinline__ bool softmax_bf16(float (&u)[2][16], float wt, float& m_ref, float& l_acc,
+                                             bf16x8 (&pa)[2][2], float& alpha) {
+  bool any_move;
+  const float bm = row_max_frame(u, wt, m_ref, l_acc, alpha, any_move);
+  const float bias = bm > -INFINITY ? -m_ref : 0.0f;  // masked u are -inf: p = 0
+  float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pr = __builtin_amdgcn_exp2f(fmaf(u[b][e], wt, bias));
+      ls[e & 3] += pr;
+      pa[b][e >> 3][e & 7] = (__bf16)pr;
+    }
+  l_acc += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+  return any_move;
+}
+
+// bf16 P.V of the channel chunks c0 and c0 + 1 of one tile, accumulated
+// straight into O: 8 v_mfma_f32_32x32x16_bf16 as two interleaved chains, the
+// V fragments (fragment (c * 2 + b) * 2 + tt of the stage) read first.
+template <int D>
+__device__ __forceinline__ void pv_bf16_pair(const uint8_t* sb, const bf16x8 (&pa)[2][2], int lane, int c0,
+                                             f32x16* o) {
+  using St = Stage<D, kPV_BF16>;
+  const bf16x8* vl = reinterpret_cast<const bf16x8*>(sb + St::offV);
+  bf16x8 vf[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) vf[j] = vl[((c0 + (j & 1)) * 4 + (j >> 1)) * 64 + lane];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int c = c0 + (j & 1), k = j >> 1;
+    o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[k >> 1][k & 1], vf[j], o[c], 0, 0, 0);
+  }
+}
+
 // The per-tile work of one wave in the general loop, as straight-line code
 // for the scheduler: scores of tile t from s0/s1, the next tile's S^T into
 // s0/s1 (both halves issued first, as two interleaved MFMA chains, so the
@@ -421,20 +480,10 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
     }
     return;
   }
-  const float bm = row_max_move<D>(u, wt, m_ref, l_acc, o, xrow, h, r);
   // bf16 P = 2^(s - m_ref) <= 2^kTau, accumulated straight into O
-  const float bias = bm > -INFINITY ? -m_ref : 0.0f;
-  float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   bf16x8 pa[2][2];
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float pr = __builtin_amdgcn_exp2f(fmaf(u[b][e], wt, bias));
-      ls[e & 3] += pr;
-      pa[b][e >> 3][e & 7] = (__bf16)pr;
-    }
-  l_acc += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+  float alpha;
+  if (softmax_bf16(u, wt, m_ref, l_acc, pa, alpha)) frame_move_o<D>(o, xrow, alpha, h, r);
   // V fragments read four MFMAs ahead of their use: the chain waits for one
   // LDS latency, not one per MFMA
   const bf16x8* vl = reinterpret_cast<const bf16x8*>(sb + St::offV);
@@ -540,8 +589,11 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
   constexpr bool kDocDma = (MASK & 2) && PV == kPV_FP8;
   const __amdgpu_buffer_rsrc_t rs_doc =
       raw_rsrc(kDocDma ? static_cast<const void*>(docb) : static_cast<const void*>(p.ks), (uint32_t)(p.n * 4));
-  auto load_tile = [&](int tt, uint8_t* sbw) __attribute__((always_inline)) {
+  auto load_k = [&](int tt, uint8_t* sbw) __attribute__((always_inline)) {
     dma_chunks_buf<St::cK, 4>(sbw, wave_u, lane, rs_k, tt * 64 * D);
+  };
+  // the rest of the stage: V, the scales, the document ids
+  auto load_v = [&](int tt, uint8_t* sbw) __attribute__((always_inline)) {
     dma_chunks_buf<St::cV, 4>(sbw + St::offV, wave_u, lane, rs_v, tt * St::vBytes);
     if (wave_u == 0) {
       // K scales by lanes 0..15 (64 keys), V scales by lanes 16.. (D
@@ -560,6 +612,10 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       pre_doc.z = base + 2 < p.n ? docb[base + 2] : -1;
       pre_doc.w = base + 3 < p.n ? docb[base + 3] : -1;
     }
+  };
+  auto load_tile = [&](int tt, uint8_t* sbw) __attribute__((always_inline)) {
+    load_k(tt, sbw);
+    load_v(tt, sbw);
   };
   auto store_doc = [&](uint8_t* sbw) __attribute__((always_inline)) {
     if (!kDocDma && (MASK & 2) && tid >= 48 && tid < 64) reinterpret_cast<int4*>(sbw + St::offDoc)[tid - 48] = pre_doc;
@@ -584,8 +640,15 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
     }
   };
 
-  constexpr bool kFast = PV == kPV_FP8;
   constexpr bool DOC = (MASK & 2) != 0;
+  // the software-pipelined loop: every fp8 P.V variant, and bf16 P.V without
+  // document ids
+  constexpr bool kFast = PV == kPV_FP8 || !DOC;
+  // bf16 P.V on the pipelined loop keeps three stages: a tile's K part is
+  // loaded two tiles ahead and its V part (with the scales) one tile ahead,
+  // so the K of tile i+2 goes into the stage whose V (tile i-1) the pending
+  // product still reads
+  constexpr bool kSplit = kFast && PV == kPV_BF16;
   // ---- prologue: tiles 0 and 1 of the schedule in stages 0 and 1 --------------
   int t = next_active(t_begin);
   int t1 = t < t_end ? next_active(t + 1) : t_end;
@@ -595,8 +658,12 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
     store_doc(smem);
   }
   if (t1 < t_end) {
-    load_tile(t1, smem + St::bytes);
-    store_doc(smem + St::bytes);
+    if constexpr (kSplit) {
+      load_k(t1, smem + St::bytes);
+    } else {
+      load_tile(t1, smem + St::bytes);
+      store_doc(smem + St::bytes);
+    }
   }
   // Document ids with fp8 P.V: the pipelined loop computes every scheduled
   // tile in every live wave with no visibility test, which holds for a tile
@@ -650,16 +717,18 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
     t2 = t2 < t_end ? next_active(t2 + 1) : t_end;
   };
   if constexpr (kFast) {
-   {
-    // ---- fp8 P.V: every scheduled tile is computed by every live wave, so
-    // the product of tile i-1 is always pending in iteration i.  The first
-    // and the last tile are peeled off the loop, which leaves its body one
-    // straight basic block for the scheduler: the pending P.V in two
-    // chunk-pair halves, each under half of this tile's score conversion,
-    // then the next tile's S^T under this tile's softmax.  With document ids
-    // the tiles before prefix_end, which some live wave does not see whole,
-    // go through the general body first; every later scheduled tile is seen
-    // whole by every live wave.
+    // ---- every scheduled tile is computed by every live wave, so the product
+    // of tile i-1 is always pending in iteration i.  The first and the last
+    // tile are peeled off the loop, which leaves its body one straight basic
+    // block for the scheduler: the pending P.V in two chunk-pair halves, each
+    // under half of this tile's score conversion, then the next tile's S^T
+    // under this tile's softmax.  fp8: the pending product's MFMAs and their
+    // dequantization into O; bf16: its MFMAs accumulate into O, after the
+    // frame move the previous softmax decided (deferred to here, so the
+    // softmax never waits for the product in flight).  With document ids
+    // (fp8) the tiles before prefix_end, which some live wave does not see
+    // whole, go through the general body first; every later scheduled tile
+    // is seen whole by every live wave.
     constexpr int NP = NC / 2;
     int stage = 0;
     if constexpr (DOC) {
@@ -673,6 +742,14 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       t1 = t2;
       t2 = t2 < t_end ? next_active(t2 + 1) : t_end;
     };
+    auto issue_loads = [&]() __attribute__((always_inline)) {
+      if constexpr (kSplit) {
+        if (t2 < t_end) load_k(t2, sp(next_stage(stage, 2)));
+        if (t1 < t_end) load_v(t1, sp(next_stage(stage, 1)));
+      } else {
+        if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+      }
+    };
     auto publish = [&]() __attribute__((always_inline)) {
       if (t2 < t_end) store_doc(sp(next_stage(stage, 2)));
       wait_vmem();
@@ -681,7 +758,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
     if (!wave_live) {
       // rows past N: the same loads and barriers, nothing computed
       while (t < t_end) {
-        if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+        issue_loads();
         publish();
         advance();
       }
@@ -689,26 +766,53 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       return;
     }
     const bool any = t < t_end;
+    // the pending product: fp8 P codes and their row factor, or bf16 P and
+    // the frame move that precedes its accumulation
     i32x8 pa_p = {0, 0, 0, 0, 0, 0, 0, 0};
     float rsc_p = 0.0f;
+    bf16x8 pb_p[2][2];
+    float alpha_p = 1.0f;
+    bool move_p = false;
     int stage_p = 0;
     float u[2][16];
+    auto softmax_p = [&]() __attribute__((always_inline)) {
+      if constexpr (PV == kPV_FP8)
+        softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
+      else
+        move_p = softmax_bf16(u, w, m_ref, l_acc, pb_p, alpha_p);
+    };
+    // the pending product, chunk pair c2 (its frame move first, for bf16)
+    auto pending_pair = [&](const uint8_t* sbp, int c2) __attribute__((always_inline)) {
+      if constexpr (PV == kPV_FP8) {
+        f32x16 p0, p1;
+        f32x32 rv;
+        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
+        pv_accum(o, c2, p0, p1, rv);
+      } else {
+        pv_bf16_pair<D>(sbp, pb_p, lane, c2, o);
+      }
+    };
+    auto pending_move = [&]() __attribute__((always_inline)) {
+      if constexpr (PV == kPV_BF16) {
+        if (move_p) frame_move_o<D>(o, xrow, alpha_p, h, r);
+      }
+    };
     if (t < t_end) {  // first tile: nothing pending
-      if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+      issue_loads();
       dump(t, s0, s1);
       const float kdb = kd_block(t);
       const int kvalid = keys_valid(t);
       half_scores<D, QK, PV, GRAN, false>(sp(stage), s0, 0, h, kdb, kvalid, false, dq, u[0]);
       half_scores<D, QK, PV, GRAN, false>(sp(stage), s1, 1, h, kdb, kvalid, false, dq, u[1]);
       if (t1 < t_end) qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
-      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
+      softmax_p();
       stage_p = stage;
       publish();
       advance();
     }
     // one iteration for a whole tile t with a successor
     auto iteration = [&]() __attribute__((always_inline)) {
-      if (t2 < t_end) load_tile(t2, sp(next_stage(stage, 2)));
+      issue_loads();
       const uint8_t* sb = sp(stage);
       const uint8_t* sbp = sp(stage_p);
       const float kdb = kd_block(t);
@@ -716,34 +820,49 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       auto scores = [&](int b_, float (&u_)[16]) __attribute__((always_inline)) {
         half_scores<D, QK, PV, GRAN, false>(sb, b_ ? s1 : s0, b_, h, kdb, 64, false, dq, u_);
       };
-      f32x16 p0, p1;
-      f32x32 rv;
-      pv_issue<D>(sbp, pa_p, rsc_p, lane, 0, p0, p1, rv);
-      scores(0, u[0]);
-      if constexpr (NP == 1) scores(1, u[1]);
-      pv_accum(o, 0, p0, p1, rv);
-      if constexpr (NP == 2) {
-        pv_issue<D>(sbp, pa_p, rsc_p, lane, 2, p0, p1, rv);
+      pending_move();
+      if constexpr (PV == kPV_FP8) {
+        f32x16 p0, p1;
+        f32x32 rv;
+        pv_issue<D>(sbp, pa_p, rsc_p, lane, 0, p0, p1, rv);
+        scores(0, u[0]);
+        if constexpr (NP == 1) scores(1, u[1]);
+        pv_accum(o, 0, p0, p1, rv);
+        if constexpr (NP == 2) {
+          pv_issue<D>(sbp, pa_p, rsc_p, lane, 2, p0, p1, rv);
+          scores(1, u[1]);
+          pv_accum(o, 2, p0, p1, rv);
+        }
+      } else {
+        // bf16: the first chunk pair's products under the score conversion
+        // (int8 QK, whose conversion is longer), the rest under the softmax
+        if constexpr (QK == kQK_INT8) pv_bf16_pair<D>(sbp, pb_p, lane, 0, o);
+        scores(0, u[0]);
         scores(1, u[1]);
-        pv_accum(o, 2, p0, p1, rv);
       }
       qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
-      softmax_fp8<D>(u, w, m_ref, l_acc, o, xrow, h, r, pa_p, rsc_p);
+      if constexpr (PV == kPV_BF16) {
+        if constexpr (QK != kQK_INT8) pv_bf16_pair<D>(sbp, pb_p, lane, 0, o);
+        if constexpr (NP == 2) pv_bf16_pair<D>(sbp, pb_p, lane, 2, o);
+      }
+      softmax_p();
       stage_p = stage;
       publish();
       advance();
     };
-    while (t1 < t_end) iteration();
-    if (t < t_end) {  // last tile: the pending product, then the tile with its P.V formed at once
+    // the pending product, one chunk pair's products in flight at a time
+    auto flush = [&]() __attribute__((always_inline)) {
       const uint8_t* sbp = sp(stage_p);
+      pending_move();
 #pragma unroll
       for (int c2 = 0; c2 < NC; c2 += 2) {
-        f32x16 p0, p1;
-        f32x32 rv;
-        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
-        pv_accum(o, c2, p0, p1, rv);
-        __builtin_amdgcn_sched_barrier(0);  // one pair's products in flight at a time
+        pending_pair(sbp, c2);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    };
+    while (t1 < t_end) iteration();
+    if (t < t_end) {  // last tile: the pending product, then the tile with its P.V formed at once
+      flush();
       const uint8_t* sb = sp(stage);
       dump(t, s0, s1);
       tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kd_block(t),
@@ -751,19 +870,10 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       publish();
       advance();
     } else if (any) {  // the single tile was also the first: its product is pending
-      const uint8_t* sbp = sp(stage_p);
-#pragma unroll
-      for (int c2 = 0; c2 < NC; c2 += 2) {
-        f32x16 p0, p1;
-        f32x32 rv;
-        pv_issue<D>(sbp, pa_p, rsc_p, lane, c2, p0, p1, rv);
-        pv_accum(o, c2, p0, p1, rv);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      flush();
     }
     __syncthreads();  // the ring is reused after
     return;
-   }
   }
   if constexpr (!kFast) {
     int stage = 0;

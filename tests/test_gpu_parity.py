@@ -197,6 +197,49 @@ def test_attention_matches_oracle(cuda, B, H, N, D, qk, pv, gran):
     _compare(out, lse, q, k, v, qk, pv, gran)
 
 
+@pytest.mark.parametrize("qk,pv,D", [("int8", "fp8", 128), ("int8", "bf16", 128), ("int8", "bf16", 64),
+                                     ("fp8", "bf16", 128), ("fp8", "bf16", 64)])
+def test_frame_moves_inside_the_loop(cuda, qk, pv, D):
+    """Scores that rise along the keys (K rows carry a growing multiple of a
+    direction every query shares) move each row's reference point 3-4 times
+    after the first tile, by more than 8 log2 units each time, so the
+    software-pipelined loop rescales O between the pending product of one tile
+    and the next (bf16 P.V: a move decided by one tile's softmax is applied
+    before the following product is added).
+
+    fp8 QK with fp8 P is left out: at scores this sharp one P code carries
+    most of a row's weight, and a last-ulp difference of an fp8 MFMA sum
+    moves it across an e4m3 rounding boundary (max-abs 0.055 against the
+    emulation, LSE within 1.2e-4); its loop is the int8 case's.  With fp8 QK
+    the tight check against the kernel-scheme emulation is left out too: one
+    row's output here follows a few keys' V and reaches magnitude 2-4, where
+    one bf16 step (0.0156) is above the tight bound."""
+    SA = _sa()
+    B, H, N = 1, 2, 1000
+    g = torch.Generator().manual_seed(123)
+    u = torch.randn(D, generator=g)
+    u /= u.norm()
+    q = (2 * math.sqrt(D) * u + torch.randn(B, H, N, D, generator=g)).bfloat16()
+    k = (torch.linspace(0, 14, N).view(1, 1, N, 1) * u + torch.randn(B, H, N, D, generator=g)).bfloat16()
+    v = torch.randn(B, H, N, D, generator=g).bfloat16()
+    # the inputs do what the test needs: block maxima past the first tile
+    # exceed the running reference point by more than 8 (log2 units)
+    kf = k.float() - k.float().mean(2, keepdim=True)
+    s = (q.float()[0, 0, ::97] @ kf[0, 0].T) / math.sqrt(D) * 1.4426950408889634
+    moves = torch.zeros(s.shape[0], dtype=torch.int32)
+    m_ref = s[:, :64].max(1).values
+    for t in range(64, N, 64):
+        bm = s[:, t:t + 64].max(1).values
+        mv = bm > m_ref + 8
+        moves += mv.int()
+        m_ref = torch.where(mv, bm, m_ref)
+    assert (moves >= 2).all(), moves
+    print(f"frame moves {qk}/{pv} D={D}", flush=True)
+    out, lse = SA.sage_forward(q.to(cuda), k.to(cuda), v.to(cuda), qk=qk, pv=pv)
+    torch.cuda.synchronize()
+    _compare(out, lse, q, k, v, qk, pv, "token", tight=qk == "int8")
+
+
 def test_quantize_known_answers_at_ties(cuda):
     """Rows whose amax makes the quantizer's multiplier exactly 1: the fp8 codes
     of every e4m3 rounding tie (ties to even) and int8 truncation toward zero are
