@@ -649,6 +649,18 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
   // so the K of tile i+2 goes into the stage whose V (tile i-1) the pending
   // product still reads
   constexpr bool kSplit = kFast && PV == kPV_BF16;
+  // Document ids: the item's scheduled tiles lie in [range.x, range.z), and
+  // with fp8 P.V the tiles before prefix_end (one past the last that some
+  // live wave does not see whole, from doc_prefix_kernel) go through the
+  // general tile body with its per-element visibility test; the pipelined
+  // loop computes every scheduled tile in every live wave with no test.
+  int prefix_end = t_begin;
+  if constexpr (DOC) {
+    const int4 range = load_uniform(p.doc_range, (int64_t)bidx * nq + qt);
+    t_begin = max(t_begin, range.x);
+    t_end = min(t_end, range.z);
+    if constexpr (kFast) prefix_end = range.y;
+  }
   // ---- prologue: tiles 0 and 1 of the schedule in stages 0 and 1 --------------
   int t = next_active(t_begin);
   int t1 = t < t_end ? next_active(t + 1) : t_end;
@@ -665,13 +677,6 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       store_doc(smem + St::bytes);
     }
   }
-  // Document ids with fp8 P.V: the pipelined loop computes every scheduled
-  // tile in every live wave with no visibility test, which holds for a tile
-  // that every live wave sees whole.  The tiles before prefix_end (one past
-  // the last that some live wave does not see whole, from doc_prefix_kernel)
-  // go through the general tile body with its per-element visibility test.
-  int prefix_end = t_begin;
-  if constexpr (kFast && DOC) prefix_end = load_uniform(p.doc_prefix, (int64_t)bidx * nq + qt);
   wait_vmem();
   __syncthreads();
   SAcc s0, s1;  // S^T of the tile about to be consumed
@@ -1100,16 +1105,18 @@ hipError_t launch_attn_d(int qk, int pv, int gran, int mask, const AttnParams& p
   return hipErrorInvalidValue;
 }
 
-// One wave per (batch, 128-row query tile): lanes scan the key tiles, the
-// scheduled ones (some row of the query tile sees a key) that some live
-// 32-row wave of the tile does not see whole (classify != 1); the result is
-// one past the last of them.  The pipelined fp8 loop of the attention kernel
-// takes the tiles from there on; the tiles before go through the general
-// tile body with its per-element visibility test.
+// One wave per (batch, 128-row query tile): lanes scan the key tiles for the
+// scheduled ones (some row of the query tile sees a key): the first and one
+// past the last of them bound the item's tile loop (no scan of the unseen
+// tiles before and after), and one past the last that some live 32-row wave
+// of the tile does not see whole (classify != 1) ends its prefix: the
+// pipelined fp8 loop of the attention kernel takes the tiles from there on,
+// the tiles before go through the general tile body with its per-element
+// visibility test.
 __global__ void __launch_bounds__(256) doc_prefix_kernel(const int4* __restrict__ kv_sum,
                                                          const int4* __restrict__ q_sum,
                                                          const int4* __restrict__ q_sum128, int nb, int nq, int nt,
-                                                         int32_t* __restrict__ prefix) {
+                                                         int4* __restrict__ range) {
   const int lane = threadIdx.x & 63;
   const int64_t item = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // wave-uniform
   if (item >= (int64_t)nb * nq) return;
@@ -1118,28 +1125,34 @@ __global__ void __launch_bounds__(256) doc_prefix_kernel(const int4* __restrict_
   int4 qs[4];
 #pragma unroll
   for (int w4 = 0; w4 < 4; ++w4) qs[w4] = q_sum[(int64_t)b * nq * 4 + qt * 4 + w4];
-  int last = -1;
+  int first = nt, last = -1, last_mixed = -1;
   for (int t = lane; t < nt; t += 64) {
     const int4 ks = kv_sum[(int64_t)b * nt + t];
     if (classify(q128, ks) == 0) continue;  // not scheduled
+    first = min(first, t);
+    last = t;
 #pragma unroll
     for (int w4 = 0; w4 < 4; ++w4) {
       if (qs[w4].z + qs[w4].w == 0) continue;  // wave past N
-      if (classify(qs[w4], ks) != 1) last = t;
+      if (classify(qs[w4], ks) != 1) last_mixed = t;
     }
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) last = max(last, __shfl_xor(last, off));
-  if (lane == 0) prefix[item] = last + 1;
+  for (int off = 32; off > 0; off >>= 1) {
+    first = min(first, __shfl_xor(first, off));
+    last = max(last, __shfl_xor(last, off));
+    last_mixed = max(last_mixed, __shfl_xor(last_mixed, off));
+  }
+  if (lane == 0) range[item] = make_int4(first, last_mixed + 1, last + 1, 0);
 }
 
 hipError_t launch_doc_prefix(const int4* kv_sum, const int4* q_sum, const int4* q_sum128, int64_t n, int nb,
-                             int32_t* prefix, hipStream_t st) {
+                             int4* range, hipStream_t st) {
   const int nq = (int)(padded_len(n) / 128);
   const int nt = (int)((n + 63) / 64);
   const int64_t waves = (int64_t)nb * nq;
   hipLaunchKernelGGL(doc_prefix_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, kv_sum, q_sum, q_sum128,
-                     nb, nq, nt, prefix);
+                     nb, nq, nt, range);
   return hipGetLastError();
 }
 
@@ -1160,10 +1173,8 @@ hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, 
     hipError_t e = launch_doc_summaries(p.doc, p.n, nb, const_cast<int4*>(p.kv_sum), const_cast<int4*>(p.q_sum),
                                         const_cast<int4*>(p.q_sum128), st);
     if (e != hipSuccess) return e;
-    if (pv == kPV_FP8) {
-      e = launch_doc_prefix(p.kv_sum, p.q_sum, p.q_sum128, p.n, nb, const_cast<int32_t*>(p.doc_prefix), st);
-      if (e != hipSuccess) return e;
-    }
+    e = launch_doc_prefix(p.kv_sum, p.q_sum, p.q_sum128, p.n, nb, const_cast<int4*>(p.doc_range), st);
+    if (e != hipSuccess) return e;
   }
   if (d == 128) return launch_attn_d<128>(qk, pv, gran, mask, p, st);
   if (d == 64) return launch_attn_d<64>(qk, pv, gran, mask, p, st);
@@ -1177,9 +1188,8 @@ AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d) {
   AttnWorkspace w;
   w.split = tail_split(items, nt);
   w.doc_off = 0;
-  // summaries (int4), then the fp8 loop's per-query-tile prefixes (int32)
-  w.part_off = ((size_t)(b * (nt + np / 32 + np / 128)) * sizeof(int4) + (size_t)(b * (np / 128)) * sizeof(int32_t) +
-                255) & ~(size_t)255;
+  // summaries (int4), then the per-query-tile scheduled ranges (int4)
+  w.part_off = ((size_t)(b * (nt + np / 32 + np / 128 + np / 128)) * sizeof(int4) + 255) & ~(size_t)255;
   const int64_t pieces = w.split.parts > 1 ? (items - w.split.whole) * w.split.parts : 0;
   w.bytes = w.part_off + (size_t)pieces * (size_t)(128 * d + 512) * sizeof(float);
   return w;

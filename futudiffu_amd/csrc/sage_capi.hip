@@ -277,7 +277,7 @@ int attn_fwd_impl(const void* q_codes, const float* q_scale, const void* k_codes
     p.kv_sum = reinterpret_cast<const int4*>(wsp + ws.doc_off);
     p.q_sum = p.kv_sum + b * nt;
     p.q_sum128 = p.q_sum + b * (sage::padded_len(n) / 32);
-    p.doc_prefix = reinterpret_cast<const int32_t*>(p.q_sum128 + b * (sage::padded_len(n) / 128));
+    p.doc_range = p.q_sum128 + b * (sage::padded_len(n) / 128);
   }
   p.qc = static_cast<const uint8_t*>(q_codes);
   p.qs = q_scale;

@@ -20,10 +20,11 @@ struct AttnParams {
   const int4* kv_sum;  // [B][nT]   (min doc, max doc, #valid, #padding) over keys < N
   const int4* q_sum;     // [B][Np/32] same over queries < N
   const int4* q_sum128;  // [B][Np/128] same over queries < N
-  // [B][Np/128], fp8 P.V with document ids: per 128-row query tile, one past
-  // the last scheduled key tile that some live wave of the tile does not see
-  // whole (0 if none)
-  const int32_t* doc_prefix;
+  // [B][Np/128] with document ids, per 128-row query tile: (first scheduled
+  // key tile, one past the last scheduled key tile that some live wave of
+  // the tile does not see whole (0 if none), one past the last scheduled key
+  // tile, 0); an item with no scheduled tile has first = nT, last = 0
+  const int4* doc_range;
   uint16_t* out;
   // element strides of out per batch, head and row: [B,H,N,D] is
   // (H*N*D, N*D, D), [B,N,H,D] is (N*H*D, D, H*D)
@@ -129,10 +130,11 @@ hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, 
 // Per-batch document-id summaries (min doc, max doc, #valid, #padding) of every
 // 64-key tile ([nb][ceil(n/64)]), 32-row block ([nb][Np/32]) and 128-row block
 // ([nb][Np/128]).
-// One past the last key tile that some live wave of each 128-row query tile
-// does not see whole, from the summaries (after launch_doc_summaries).
+// The scheduled key-tile range of each 128-row query tile and one past the
+// last key tile that some live wave of it does not see whole (the doc_range
+// entries), from the summaries (after launch_doc_summaries).
 hipError_t launch_doc_prefix(const int4* kv_sum, const int4* q_sum, const int4* q_sum128, int64_t n, int nb,
-                             int32_t* prefix, hipStream_t st);
+                             int4* range, hipStream_t st);
 hipError_t launch_doc_summaries(const int32_t* doc, int64_t n, int nb, int4* kv_sum, int4* q_sum, int4* q_sum128,
                                 hipStream_t st);
 // Workspace of one attention call: the doc-id summaries, then the partial

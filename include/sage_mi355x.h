@@ -166,8 +166,9 @@ int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* 
 
 /* Bytes of device workspace sage_attn_fwd needs for B x H heads of N tokens
  * of dimension D: per-batch (min doc, max doc, #valid, #padding) summaries of
- * every 64-key tile and 32- and 128-row query block (written and used when
- * doc_ids is given), then the fp32 partial results of the key-tile pieces of
+ * every 64-key tile and 32- and 128-row query block and the scheduled
+ * key-tile range of every 128-row query block (written and used when doc_ids
+ * is given), then the fp32 partial results of the key-tile pieces of
  * the 128-row items that an unmasked launch splits (the items past the last
  * whole round of 512 resident workgroups).  No reference counterpart (the
  * Triton launch needs no workspace). */
