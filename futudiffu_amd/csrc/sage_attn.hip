@@ -355,6 +355,67 @@ __device__ __forceinline__ float row_max_move(float (&u)[2][16], float wt, float
   return bm;
 }
 
+// The exp / pack part of the fp8 softmax for fp8 QK (after the frame decision
+// for block max bm: P codes into pa, the row factor into rsc, the row sum into
+// l), with the next tile's S^T (K of stage sb_next) issued among its vector
+// work: the MFMAs of the two halves (their chains alternate) in four groups,
+// each followed by the exp / pack work of 8 of the lane's 32 scores, with
+// scheduling fences between the groups, so the wave keeps issuing vector
+// instructions while its matrix core forms the next S^T.  K fragments are
+// read two MFMAs ahead.
+template <int D>
+__device__ __forceinline__ void softmax_fp8_exp_qk(const float (&u)[2][16], float wt, float bm, float m_ref,
+                                                   float& l_acc, i32x8& pa, float& rsc, const uint8_t* sb_next,
+                                                   const i32x4* qf, int lane, f32x16& a0, f32x16& a1) {
+  constexpr int NC = D / 32;
+  constexpr int kM = NC;  // MFMA i: half i & 1, channels 64 (i >> 1) .. + 63
+  const i32x4* kl = reinterpret_cast<const i32x4*>(sb_next);
+  i32x4 kf[kM][2];
+  auto read = [&](int i) __attribute__((always_inline)) {
+    const int b = i & 1, c = (i >> 1) * 2;
+    kf[i][0] = kl[(b * NC + c) * 64 + lane];
+    kf[i][1] = kl[(b * NC + c + 1) * 64 + lane];
+  };
+  auto mfma = [&](int i) __attribute__((always_inline)) {
+    const int b = i & 1, c = (i >> 1) * 2;
+    f32x16& acc = b ? a1 : a0;
+    const i32x8 bq = {qf[c][0], qf[c][1], qf[c][2], qf[c][3], qf[c + 1][0], qf[c + 1][1], qf[c + 1][2], qf[c + 1][3]};
+    const i32x8 ka = {kf[i][0][0], kf[i][0][1], kf[i][0][2], kf[i][0][3],
+                      kf[i][1][0], kf[i][1][1], kf[i][1][2], kf[i][1][3]};
+    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka, bq, i < 2 ? f32x16{0} : acc, 0, 0, 0, 0, 0, 0);
+  };
+  read(0);
+  if (kM > 1) read(1);
+  const bool row_live = bm > -INFINITY;
+  rsc = row_live ? __builtin_amdgcn_exp2f(bm - m_ref) * (1.0f / kFp8Max) : 0.0f;
+  const float bias = row_live ? (kLog2Fp8Max - bm) : 0.0f;  // masked u are -inf: e = 0
+  float es[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = g * kM / 4; i < (g + 1) * kM / 4; ++i) {
+      mfma(i);
+      if (i + 2 < kM) read(i + 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // scores of half g >> 1, rows 8j + 4h + i for j = 2 (g & 1) .. + 1
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int b = g >> 1, j = 2 * (g & 1) + jj;
+      float e4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e4[i] = __builtin_amdgcn_exp2f(fmaf(u[b][4 * j + i], wt, bias));
+        es[i] += e4[i];
+      }
+      pa[4 * b + j] = (int)pack_fp8x4(e4[0], e4[1], e4[2], e4[3]);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  l_acc = fmaf(rsc, (es[0] + es[1]) + (es[2] + es[3]), l_acc);
+}
+
 template <int D>
 __device__ __forceinline__ void softmax_fp8(float (&u)[2][16], float wt, float& m_ref, float& l_acc, f32x16* o,
                                             float* xrow, int h, int r, i32x8& pa, float& rsc) {
@@ -834,6 +895,10 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
         if constexpr (NP == 1) scores(1, u[1]);
         pv_accum(o, 0, p0, p1, rv);
         if constexpr (NP == 2) {
+          // fp8 QK: the second pair's products and factors only once the
+          // first pair's are consumed (with the next S^T formed later, both
+          // at once would not fit the registers)
+          if constexpr (QK == kQK_FP8) __builtin_amdgcn_sched_barrier(0);
           pv_issue<D>(sbp, pa_p, rsc_p, lane, 2, p0, p1, rv);
           scores(1, u[1]);
           pv_accum(o, 2, p0, p1, rv);
@@ -845,12 +910,23 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
         scores(0, u[0]);
         scores(1, u[1]);
       }
-      qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
-      if constexpr (PV == kPV_BF16) {
-        if constexpr (QK != kQK_INT8) pv_bf16_pair<D>(sbp, pb_p, lane, 0, o);
-        if constexpr (NP == 2) pv_bf16_pair<D>(sbp, pb_p, lane, 2, o);
+      if constexpr (PV == kPV_FP8 && QK == kQK_FP8 && D == 128) {
+        // fp8 QK, D = 128: the frame decision ends a scheduling region (its
+        // rare O rescale is a branch); the next tile's S^T goes after it,
+        // among the exp / pack work of this tile (A/B at 1x30x4416x128
+        // fp8/fp8: 234.7 -> 230.7 us and 240.3 -> 235.7 us; with int8 QK the
+        // same order measured 247.7 -> 250.8 us: the other wave of the SIMD
+        // already covers the QK^T burst)
+        const float bm = row_max_move<D>(u, w, m_ref, l_acc, o, xrow, h, r);
+        softmax_fp8_exp_qk<D>(u, w, bm, m_ref, l_acc, pa_p, rsc_p, sp(next_stage(stage, 1)), qf, lane, s0, s1);
+      } else {
+        qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
+        if constexpr (PV == kPV_BF16) {
+          if constexpr (QK != kQK_INT8) pv_bf16_pair<D>(sbp, pb_p, lane, 0, o);
+          if constexpr (NP == 2) pv_bf16_pair<D>(sbp, pb_p, lane, 2, o);
+        }
+        softmax_p();
       }
-      softmax_p();
       stage_p = stage;
       publish();
       advance();

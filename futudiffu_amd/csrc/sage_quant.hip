@@ -842,6 +842,49 @@ __global__ void __launch_bounds__(256) quantize_k_kernel(const uint16_t* __restr
   }
 }
 
+// Waits until every chunk flag of head bh shows this call's epoch, for at most
+// spin_limit rounds of s_sleep; returns whether they all did (uniform).
+__device__ __forceinline__ bool wait_head_flags(const uint64_t* __restrict__ hf, int64_t nch, uint64_t epoch,
+                                                int spin_limit, int tid) {
+  uint64_t f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+  bool ready = __syncthreads_and(f == epoch);
+  for (int r = 0; !ready && r < spin_limit; ++r) {
+    __builtin_amdgcn_s_sleep(32);
+    f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+    ready = __syncthreads_and(f == epoch);
+  }
+  return ready;
+}
+
+// Thread tid's partial sum of the head mean (for head_mean): from the
+// published chunk sums (read with agent-scope relaxed atomic loads, the
+// coherence point) when ready, else from the head's chunk sums formed here
+// with the same arithmetic and order (chunk_colsum; LDS from lds).
+template <int D, bool PROD>
+__device__ __forceinline__ double head_sum_part(bool ready, const HeadRows<D, PROD>& src, const ProdArgs& prod,
+                                                int bh, int64_t n, int64_t nch, const double* __restrict__ ksum_part,
+                                                uint8_t* lds, int tid) {
+  constexpr int TPC = 256 / D;
+  double s = 0.0;
+  if (ready) {
+    double mt[kMeanLoads];
+    load_chunk_sums<D, true>(ksum_part + (int64_t)bh * nch * D + tid % D, nch, tid, mt);
+    s = mean_sum<D>(mt, nch, tid);
+  } else {
+    double(*msum)[D] = reinterpret_cast<double(*)[D]>(lds);
+    double* ksw = reinterpret_cast<double*>(lds + TPC * D * 8 + D * 4);
+#pragma unroll 1
+    for (int64_t c = 0; c < nch; ++c) {
+      const double cs = chunk_colsum<D, PROD, 2>(src.k, src.stride, src.row0, prod, c, n, ksw, tid);
+      if (tid < D) msum[0][tid] = cs;  // chunk c's column sums
+      __syncthreads();
+      if (c % TPC == tid / D) s += msum[0][tid % D];
+      __syncthreads();
+    }
+  }
+  return s;
+}
+
 // One-kernel form with smoothing (not used under stream capture: the epoch is
 // a launch argument).  1D grid, units in dispatch order:
 //   [0, nsum)   K column sums of chunk u / BH of head u % BH; each publishes
@@ -978,15 +1021,154 @@ __global__ void __launch_bounds__(256) quantize_one_kernel(
                                         tid);
 }
 
+// Single-read form with smoothing, for heads whose chunks are 256 tokens
+// (k_sum_tokens(n, D) == 256; not used under stream capture, nor with the
+// producer, whose K units would hold too many registers).  1D grid, head
+// after head: the head's nch K units, then its 2 * nblk Q and V block units.
+// A K unit loads its 256 tokens once into registers (four 64-token blocks in
+// the lane layout of rows_load), adds their fp64 column sums in chunk_colsum's
+// order, publishes them and its chunk flag as the column-sum units of
+// quantize_one_kernel do, waits for the head's flags (wait_head_flags; after
+// a bounded wait it forms the head's chunk sums itself and loads its tokens
+// again), then smooths and quantizes the blocks it holds (those below Np).  K is read once:
+// a head's K units are consecutive in dispatch order, so every unit a waiting
+// one depends on is dispatched before any later head's work, and the bounded
+// wait covers the rest.
+template <int D, int QK, int PV, int GRAN, bool PROD>
+__global__ void __launch_bounds__(256) quantize_fused_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t bhn,
+    int64_t n, int64_t np, float fold, double* __restrict__ ksum_part, uint64_t* __restrict__ flags,
+    uint64_t epoch, int spin_limit, uint8_t* __restrict__ qc, float* __restrict__ qs, uint8_t* __restrict__ kc,
+    float* __restrict__ ks, uint8_t* __restrict__ vout, float* __restrict__ vs, uint16_t* __restrict__ kmean,
+    ProdArgs prod) {
+  using L = QuantLds<D, PV>;
+  constexpr int LPR = D / 8;
+  constexpr int RPP = 256 / LPR;
+  constexpr int PASSES = 64 / RPP;
+  constexpr int TPC = 256 / D;
+  static_assert(TPC * D * 8 + D * 4 + 4 * D * 8 <= L::kBytes, "K role scratch fits");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kTotal];
+  unsigned* blk_amax = reinterpret_cast<unsigned*>(lds + L::kAmax);
+  const int tid = threadIdx.x;
+  const int64_t nch = k_sum_chunks(n, D);
+  const int64_t nblk = np / 64;
+  const int64_t per_head = nch + 2 * nblk;
+  const int bh = (int)(blockIdx.x / per_head);
+  const int64_t u = blockIdx.x - (int64_t)bh * per_head;
+  const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+  if (u >= nch) {
+    const int role = (int)((u - nch) & 1);
+    const int64_t blk = (u - nch) >> 1;
+    const int64_t tok0 = blk * 64;
+    if (role == 1) {
+      v_block<D, PV>(src.v, src.stride, tok0, n, blk, bh, np, vout, vs, lds, tid);
+      return;
+    }
+    if (GRAN == kGRAN_BLOCK64) {
+      if (tid == 0) *blk_amax = 0u;
+      __syncthreads();
+    }
+    const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+    rows_block<D, QK, GRAN, PROD>(src.q, src.stride, src.row0, prod.qw, prod, tok0, n, fold,
+                                  qc + (int64_t)bh * np * D, qs + sco, blk_amax, tid);
+    return;
+  }
+  // ---- K of one 256-token chunk, read once ----
+  const int64_t ch = u;
+  const int64_t tok0 = ch * 256;
+  const int wave = tid >> 6, c8 = tid % LPR, rr = tid / LPR;
+  uint4 w[4][PASSES];
+  // the chunk's 256 tokens (through the producer for PROD)
+  auto load_chunk = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) rows_load<D>(src.k, src.stride, tok0 + 64 * b, n, tid, w[b]);
+    if constexpr (PROD) {
+      float kn[8];
+      load_w8(prod.kw, c8, kn);
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+          f32x4 fr[4];
+          load_freqs<D>(prod.freqs, src.row0 + min(tok0 + 64 * b + rr + ps * RPP, n - 1), c8, fr);
+          w[b][ps] = rms_rope8<D>(w[b][ps], kn, fr, prod.eps);  // zero rows stay zero
+        }
+    }
+  };
+  load_chunk();
+  if (GRAN == kGRAN_BLOCK64 && tid < 4) blk_amax[tid] = 0u;
+  {
+    // column sums: each lane adds its tokens rr, rr + RPP, ... in order, then
+    // the lanes of a column in a fixed tree, then the 4 waves in order (the
+    // order of chunk_colsum)
+    double cs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cs[e] = 0.0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int ps = 0; ps < PASSES; ++ps) {
+        float x[8];
+        unpack8(w[b][ps], x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cs[e] += (double)x[e];
+        __builtin_amdgcn_sched_barrier(0);  // one piece at a time: the held blocks stay packed
+      }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) cs[e] += __shfl_xor(cs[e], off);
+    double* ksw = reinterpret_cast<double*>(lds + TPC * D * 8 + D * 4);
+    if ((tid & 63) < LPR) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ksw[wave * D + c8 * 8 + e] = cs[e];
+    }
+    __syncthreads();
+    const double col = tid < D ? (ksw[tid] + ksw[D + tid]) + (ksw[2 * D + tid] + ksw[3 * D + tid]) : 0.0;
+    if (tid < D)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(ksum_part) + ((int64_t)bh * nch + ch) * D + tid,
+                         __builtin_bit_cast(uint64_t, col), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vmem();
+    __syncthreads();  // also ends every read of ksw
+    if (tid == 0) __hip_atomic_store(&flags[(int64_t)bh * nch + ch], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const bool ready = wait_head_flags(flags + (int64_t)bh * nch, nch, epoch, spin_limit, tid);
+  const double s = head_sum_part<D, PROD>(ready, src, prod, bh, n, nch, ksum_part, lds, tid);
+  if (!ready) load_chunk();  // (rare) the tokens again: none stay in registers while the sums are formed
+  head_mean<D>(s, n, reinterpret_cast<double(*)[D]>(lds), reinterpret_cast<float*>(lds + TPC * D * 8),
+               ch == 0 ? kmean + (int64_t)bh * D : nullptr, tid);
+  const float* mu = reinterpret_cast<const float*>(lds + TPC * D * 8);
+  const int64_t co = (int64_t)bh * np * D;
+  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int64_t t0 = tok0 + 64 * b;
+    __builtin_amdgcn_sched_barrier(0);  // one block at a time
+    if (t0 >= np) break;  // uniform: blocks past the padded length hold no codes
+    if (t0 + 64 <= n)
+      rows_quant<D, QK, GRAN, false, false>(w[b], src.row0, prod.kw, prod, t0, n, 1.0f, mu, kc + co, ks + sco,
+                                            &blk_amax[b], tid);
+    else
+      rows_quant<D, QK, GRAN, false, true>(w[b], src.row0, prod.kw, prod, t0, n, 1.0f, mu, kc + co, ks + sco,
+                                           &blk_amax[b], tid);
+  }
+}
+
 // Quantization launch form: one kernel unless the stream is capturing
-// (default), or forced by SAGE_QUANT_PATH: "two" (two kernels), "fallback"
-// (one kernel whose K workgroups form the chunk sums themselves; for tests).
-enum { kQuantAuto = 0, kQuantTwoKernels = 1, kQuantOneFallback = 2 };
+// (default: the single-read form for large launches whose heads have
+// 256-token chunks, else the lagged form), or forced by SAGE_QUANT_PATH:
+// "two" (two kernels), "lagged" (the lagged one-kernel form), "fused" (the
+// single-read form wherever it applies), "fallback" (the default one-kernel
+// form with K workgroups that skip the wait and form the chunk sums
+// themselves; for tests).
+enum { kQuantAuto = 0, kQuantTwoKernels = 1, kQuantOneFallback = 2, kQuantLagged = 3, kQuantFused = 4 };
 int quant_path() {
   const char* e = std::getenv("SAGE_QUANT_PATH");
   if (e == nullptr) return kQuantAuto;
   if (std::strcmp(e, "two") == 0) return kQuantTwoKernels;
   if (std::strcmp(e, "fallback") == 0) return kQuantOneFallback;
+  if (std::strcmp(e, "lagged") == 0) return kQuantLagged;
+  if (std::strcmp(e, "fused") == 0) return kQuantFused;
   return kQuantAuto;
 }
 
@@ -1004,12 +1186,13 @@ struct QuantCall {
   float* vs;
   uint16_t* kmean;
   ProdArgs prod;
-  int path;  // kQuantAuto, kQuantTwoKernels, kQuantOneFallback
+  int path;  // kQuantAuto, kQuantTwoKernels, kQuantOneFallback, kQuantLagged
 };
 
 // A 64-bit value never passed to an earlier launch of this process: a clock
 // reading at first use (distinct across processes) plus a call counter.
 constexpr int64_t kLagUnits = 2048;  // Q and V workgroups dispatched ahead of the first K workgroup
+constexpr int64_t kFusedMinTokens = 1 << 18;  // head tokens (B * H * N) from which the single-read form runs
 
 uint64_t next_epoch() {
   static std::atomic<uint64_t> counter{0};
@@ -1029,6 +1212,20 @@ hipError_t launch_quantize_t(const QuantCall& a, hipStream_t st) {
     if (a.path != kQuantTwoKernels && cap == hipStreamCaptureStatusNone) {
       const int64_t nch = k_sum_chunks(a.n, D);
       uint64_t* flags = reinterpret_cast<uint64_t*>(a.ws + a.bh * nch * D);
+      const int spin = a.path == kQuantOneFallback ? 0 : 4096;
+      // the single-read form for launches of at least kFusedMinTokens head
+      // tokens (measured: 4 x 30 x 4352 x 128 135.0 -> 118.8 us; at 30 x
+      // 4416 its halved occupancy and each K unit's serial wait make it slower,
+      // 31.3 -> 37.5 us), when a head's chunks are 256 tokens
+      const bool fits = !PROD && k_sum_tokens(a.n, D) == 256;
+      const bool big = a.bh * a.n >= kFusedMinTokens;
+      if (fits && (a.path == kQuantFused || (a.path != kQuantLagged && big))) {
+        const int64_t grid = a.bh * (nch + 2 * nblk);
+        hipLaunchKernelGGL((quantize_fused_kernel<D, QK, PV, GRAN, PROD>), dim3((unsigned)grid), dim3(256), 0, st,
+                           a.q, a.k, a.v, a.bh, a.n, np, a.fold, a.ws, flags, next_epoch(), spin, a.qc, a.qs, a.kc,
+                           a.ks, a.vout, a.vs, a.kmean, a.prod);
+        return hipGetLastError();
+      }
       const int64_t grid = nch * a.bh + 3 * nblk * a.bh;
       hipLaunchKernelGGL((quantize_one_kernel<D, QK, PV, GRAN, PROD>), dim3((unsigned)grid), dim3(256), 0, st, a.q,
                          a.k, a.v, a.bh, a.n, np, a.fold, a.ws, flags, next_epoch(),

@@ -1,13 +1,17 @@
 """The quantization's launch forms give the same bits.
 
-With smoothing, ``sage_quantize_qkv`` runs one kernel: its K blocks wait for
-their head's column sums through flags tagged with a per-call epoch, and after
-a bounded wait they form the sums themselves.  Under stream capture it runs
-two kernels instead (a captured epoch would repeat on every replay).
-``SAGE_QUANT_PATH`` forces a form from the host: ``two`` (two kernels) or
-``fallback`` (one kernel whose K blocks skip the wait and form the sums
-themselves), so each form is checked against the others bit for bit, and the
-default against the oracle.
+With smoothing, ``sage_quantize_qkv`` runs one kernel: its K workgroups wait
+for their head's column sums through flags tagged with a per-call epoch, and
+after a bounded wait they form the sums themselves.  Large launches whose heads
+have 256-token chunks read K once (each K workgroup holds its chunk while it
+waits, the single-read form); the others use the lagged form, whose K blocks
+read K a second time.  Under stream capture it runs two kernels instead (a
+captured epoch would repeat on every replay).  ``SAGE_QUANT_PATH`` forces a
+form from the host: ``two`` (two kernels), ``lagged`` (the lagged one-kernel
+form), ``fused`` (the single-read form wherever it applies) or ``fallback``
+(the default one-kernel form with K workgroups that skip the wait and form the
+sums themselves), so each form is checked against the others bit for bit, and
+the default against the oracle.
 
 Heads of 20000 tokens take 1024-token chunks at D = 128 (512 at D = 64), the
 widening that keeps every head within 24 (48) chunk sums.
@@ -22,12 +26,13 @@ from oracle import sage_oracle as O
 
 pytestmark = pytest.mark.gpu
 
-PATHS = (None, "two", "fallback")
+PATHS = (None, "two", "fallback", "lagged", "fused")
 FIELDS = ("q_codes", "q_scale", "k_codes", "k_scale", "v_op", "v_scale", "k_mean")
 
 CASES = [
     # (B, H, N, D, qk, pv, gran)
     (1, 30, 4416, 128, "int8", "fp8", "token"),
+    (4, 30, 4352, 128, "int8", "fp8", "token"),  # 2040 single-read K workgroups: more than stay resident
     (1, 2, 20000, 128, "int8", "fp8", "token"),
     (1, 2, 20000, 64, "fp8", "bf16", "token"),
     (2, 3, 1000, 128, "fp8", "fp8", "block64"),
