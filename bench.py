@@ -64,6 +64,9 @@ def parse():
     ap.add_argument("--stream-calibration", action="store_true",
                     help="instead of the benchmark, time a 2:1 read/write stream at the quantization's "
                          "traffic and at 1 GiB, warm and cold")
+    ap.add_argument("--isa-probe", action="store_true",
+                    help="instead of the benchmark, measure gfx950 issue costs and MFMA/VALU co-execution "
+                         "with the probes of futudiffu_amd/libsage_probe.so")
     ap.add_argument("--all-configs", action="store_true",
                     help="one JSON line per benchmark configuration instead of the headline line")
     ap.add_argument("--cases", default="",
@@ -331,6 +334,42 @@ def stream_calibration(args):
         for cold in (False, True):
             out[f"{label}_{'cold' if cold else 'warm'}_GBs"] = round(stream_rate(nbytes, cold), 1)
     print(json.dumps(out), flush=True)
+
+
+def isa_probe(args):
+    """Issue cost per wave-instruction (s_memtime ticks = shader clock) at one
+    and two waves per SIMD, and the co-execution of MFMA and FMA streams on
+    one SIMD, from libsage_probe.so (csrc/sage_probe.hip)."""
+    import ctypes
+    torch.cuda.init()
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "futudiffu_amd", "libsage_probe.so")
+    lib = ctypes.CDLL(path)
+    for fn in ("sage_probe_last_error", "sage_probe_issue_name", "sage_probe_coexec_variant", "sage_probe_coexec_mode"):
+        getattr(lib, fn).restype = ctypes.c_char_p
+    lib.sage_probe_issue_name.argtypes = [ctypes.c_int]
+    lib.sage_probe_coexec_variant.argtypes = [ctypes.c_int]
+    lib.sage_probe_coexec_mode.argtypes = [ctypes.c_int]
+    for fn in ("sage_probe_issue", "sage_probe_coexec"):
+        getattr(lib, fn).argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.c_int]
+    ni = lib.sage_probe_issue_count()
+    buf = (ctypes.c_double * (2 * ni))()
+    if lib.sage_probe_issue(buf, 2 * ni) < 0:
+        raise RuntimeError(lib.sage_probe_last_error().decode())
+    issue = {lib.sage_probe_issue_name(i).decode(): {"1_wave_per_simd": round(buf[2 * i], 2),
+                                                     "2_waves_per_simd": round(buf[2 * i + 1], 2)}
+             for i in range(ni)}
+    nc = lib.sage_probe_coexec_count()
+    cbuf = (ctypes.c_double * (2 * nc))()
+    if lib.sage_probe_coexec(cbuf, 2 * nc) < 0:
+        raise RuntimeError(lib.sage_probe_last_error().decode())
+    coexec = [{"variant": lib.sage_probe_coexec_variant(i).decode(), "mode": lib.sage_probe_coexec_mode(i).decode(),
+               "waves_0_3_ticks_per_iter": round(cbuf[2 * i], 1), "waves_4_7_ticks_per_iter": round(cbuf[2 * i + 1], 1)}
+              for i in range(nc)]
+    print(json.dumps({"isa_probe": "gfx950", "unit": "s_memtime ticks (shader clock)",
+                      "issue_ticks_per_wave_instruction": issue,
+                      "coexec_note": "per iteration: 4 MFMA pairs and 4x the FMA count per pair; waves w and w+4 "
+                                     "share SIMD w",
+                      "coexec": coexec}), flush=True)
 
 
 def _case_inputs(c, dev, seed=0):
@@ -643,6 +682,9 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args)
+        return
+    if args.isa_probe:
+        isa_probe(args)
         return
     if args.stream_calibration:
         stream_calibration(args)

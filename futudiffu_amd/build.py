@@ -3,7 +3,9 @@
 Compiles the HIP sources under ``csrc/`` with ``hipcc`` into one in-tree
 shared library.  Packed fp32 VALU instructions are disabled
 (``-packed-fp32-ops``); no fast-math flags are used, so fp32 division stays
-correctly rounded, which the quantization codes depend on.
+correctly rounded, which the quantization codes depend on.  The issue-cost
+probes behind ``bench.py --isa-probe`` go into a library of their own,
+libsage_probe.so.
 """
 
 from __future__ import annotations
@@ -19,6 +21,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libsage_mi355x.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 SOURCES = ["sage_quant.hip", "sage_attn.hip", "sage_mask.hip", "sage_bwd.hip", "sage_capi.hip"]
+PROBE_SOURCE = "sage_probe.hip"
+PROBE_LIB_PATH = os.path.join(HERE, "libsage_probe.so")
 ARCH = "gfx950"
 
 
@@ -37,12 +41,23 @@ def flags() -> list[str]:
     ]
 
 
+def _link(cc: str, objs: list[str], tmp: str, path: str) -> None:
+    tmp_lib = os.path.join(tmp, os.path.basename(path))
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    shutil.copyfile(tmp_lib, path + ".tmp")
+    os.replace(path + ".tmp", path)
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every source and link LIB_PATH atomically; returns its path."""
+    """Compile every source and link LIB_PATH (and PROBE_LIB_PATH) atomically;
+    returns LIB_PATH."""
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="sage_build_") as tmp:
         objs = []
-        for src in SOURCES:
+        for src in SOURCES + [PROBE_SOURCE]:
             obj = os.path.join(tmp, src + ".o")
             cmd = [cc, *flags(), "-c", os.path.join(CSRC, src), "-o", obj]
             if verbose:
@@ -51,13 +66,8 @@ def build(verbose: bool = False) -> str:
             if res.returncode != 0:
                 raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
             objs.append(obj)
-        tmp_lib = os.path.join(tmp, LIB_NAME)
-        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib]
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"link failed:\n{res.stderr}")
-        shutil.copyfile(tmp_lib, LIB_PATH + ".tmp")
-        os.replace(LIB_PATH + ".tmp", LIB_PATH)
+        _link(cc, objs[:-1], tmp, LIB_PATH)
+        _link(cc, objs[-1:], tmp, PROBE_LIB_PATH)
     return LIB_PATH
 
 
