@@ -55,8 +55,11 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 // t0 + l and t0 + 64 + l, then wave-wide min / max / sums.
 __global__ void __launch_bounds__(256) doc_summary_kernel(const int32_t* __restrict__ doc, int64_t n, int64_t np,
                                                           int nb, int nt, int4* __restrict__ kv_sum,
-                                                          int4* __restrict__ q_sum, int4* __restrict__ q_sum128) {
+                                                          int4* __restrict__ q_sum, int4* __restrict__ q_sum128,
+                                                          int4* __restrict__ heavy) {
   const int64_t nq32 = np / 32, nq128 = np / 128;
+  // the list of split query tiles that doc_prefix_kernel fills starts empty
+  if (heavy != nullptr && blockIdx.x == 0 && threadIdx.x == 0) heavy[0] = make_int4(0, 0, 0, 0);
   const int lane = threadIdx.x & 63;
   const int64_t per_b = nt + nq32 + nq128;
   const int64_t total = (int64_t)nb * per_b;
@@ -568,8 +571,10 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
 // DUMP (int8 QK only) also stores every S^T accumulator pair this loop
 // consumes into p.s_dump, at the point where it is consumed.
 template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false>
-__device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, int bh, int qt, int t_begin,
-                                           int t_end, f32x16* o, float& m_ref, float& l_acc) {
+__device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, int bh, int qt, int t_begin,
+                                           int t_end, f32x16* o, float& m_ref, float& l_acc,
+                                           bool skip_listed = false) {
+  bool listed = false;
   using St = Stage<D, PV>;
   using SM = Smem<D, PV>;
   using SAcc = typename SAccT<QK>::type;
@@ -718,6 +723,12 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
   int prefix_end = t_begin;
   if constexpr (DOC) {
     const int4 range = load_uniform(p.doc_range, (int64_t)bidx * nq + qt);
+    // a listed split query tile belongs to one of the first workgroups
+    // (doc_prefix_kernel): here it runs no tile and the caller stores
+    // nothing.  No branch precedes the item's other loads, so they stay
+    // beside the range's.
+    listed = skip_listed && range.w != 0;
+    t_begin = listed ? t_end : t_begin;
     t_begin = max(t_begin, range.x);
     t_end = min(t_end, range.z);
     if constexpr (kFast) prefix_end = range.y;
@@ -829,7 +840,7 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
         advance();
       }
       __syncthreads();
-      return;
+      return !listed;
     }
     const bool any = t < t_end;
     // the pending product: fp8 P codes and their row factor, or bf16 P and
@@ -954,13 +965,13 @@ __device__ __forceinline__ void item_tiles(const AttnParams& p, uint8_t* smem, i
       flush();
     }
     __syncthreads();  // the ring is reused after
-    return;
+    return !listed;
   }
   if constexpr (!kFast) {
     int stage = 0;
     while (t < t_end) general_step(stage);
   }
-  return;
+  return !listed;
 }
 
 constexpr int kRawBufferWord3 = 0x00020000;  // word 3 of a raw (untyped) buffer resource, gfx9 family
@@ -1044,6 +1055,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   const int nq = (int)(p.np / kRowsPerWG);
 
   int bh, qt;
+  bool skip_listed = false;  // document ids: this workgroup leaves a listed split query tile to the first ones
   if constexpr (MASK == 0) {
     // Unmasked: items in head-major order.  Workgroups [0, n_whole) take whole
     // items, dealt to XCDs (workgroup i runs on XCD i % 8) in contiguous
@@ -1069,9 +1081,27 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
     bh = (int)(pos / nq);
     qt = (int)(pos % nq);
   } else {
-    item_of(blockIdx.x, (int)gridDim.x, p.bh, nq, p.light_last, bh, qt);
+    const int id = blockIdx.x, total = gridDim.x;
+    if constexpr ((MASK & 2) != 0) {
+      // the first heavy_max * h workgroups: head id % h of listed split query
+      // tile id / h (doc_prefix_kernel); the others run the usual order and
+      // leave the listed items to them
+      const int reserved = p.heavy_max * p.h;
+      if (id < reserved) {
+        const int e = id / p.h;
+        if (e >= load_uniform(&p.heavy[0].x, 0)) return;
+        const int it = load_uniform(&p.heavy[1 + e].x, 0);
+        bh = (it / nq) * p.h + id % p.h;
+        qt = it % nq;
+      } else {
+        item_of(id - reserved, total - reserved, p.bh, nq, p.light_last, bh, qt);
+        skip_listed = true;
+      }
+    } else {
+      item_of(id, total, p.bh, nq, p.light_last, bh, qt);
+    }
   }
-  item_tiles<D, QK, PV, GRAN, MASK, DUMP>(p, smem, bh, qt, 0, p.nt, o, m_ref, l_acc);
+  if (!item_tiles<D, QK, PV, GRAN, MASK, DUMP>(p, smem, bh, qt, 0, p.nt, o, m_ref, l_acc, skip_listed)) return;
   store_rows_final<D, PV>(p, smem, bh, qt, o, m_ref, l_acc);
 }
 
@@ -1154,7 +1184,9 @@ template <int D, int QK, int PV, int GRAN>
 hipError_t launch_attn_g(int mask, const AttnParams& p, hipStream_t st) {
   const int64_t items = (int64_t)p.bh * (p.np / kRowsPerWG);
   const int64_t n_split = mask == 0 ? items - p.n_whole : 0;
-  const dim3 grid((unsigned)(mask == 0 ? p.n_whole + n_split * p.split_parts : items));
+  // with document ids the first heavy_max * h workgroups take the listed split query tiles
+  const dim3 grid((unsigned)(mask == 0 ? p.n_whole + n_split * p.split_parts
+                                       : items + ((mask & 2) ? (int64_t)p.heavy_max * p.h : 0)));
   // the accumulator dump exists for the int8 QK, per-token, unmasked kernels
   constexpr bool kDumpable = QK == kQK_INT8 && GRAN == kGRAN_TOKEN;
   if (p.s_dump != nullptr) {
@@ -1189,10 +1221,19 @@ hipError_t launch_attn_d(int qk, int pv, int gran, int mask, const AttnParams& p
 // pipelined fp8 loop of the attention kernel takes the tiles from there on,
 // the tiles before go through the general tile body with its per-element
 // visibility test.
+// A query tile whose live waves see different key-tile ranges (a document
+// boundary inside the tile) runs the union of those ranges through the
+// general body and is the longest item of its launch; up to heavy_max such
+// tiles per launch are listed (heavy[1 + e].x = b * nq + qt, heavy[0].x the
+// count, by an atomic counter) and flagged (range.w = 1), and the attention
+// kernel's first workgroups take them, so they do not end the launch.  The
+// list's order depends on the atomics, not the results: each item is computed
+// the same way whichever workgroup takes it.
 __global__ void __launch_bounds__(256) doc_prefix_kernel(const int4* __restrict__ kv_sum,
                                                          const int4* __restrict__ q_sum,
                                                          const int4* __restrict__ q_sum128, int nb, int nq, int nt,
-                                                         int4* __restrict__ range) {
+                                                         int4* __restrict__ range, int4* __restrict__ heavy,
+                                                         int heavy_max) {
   const int lane = threadIdx.x & 63;
   const int64_t item = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // wave-uniform
   if (item >= (int64_t)nb * nq) return;
@@ -1202,6 +1243,7 @@ __global__ void __launch_bounds__(256) doc_prefix_kernel(const int4* __restrict_
 #pragma unroll
   for (int w4 = 0; w4 < 4; ++w4) qs[w4] = q_sum[(int64_t)b * nq * 4 + qt * 4 + w4];
   int first = nt, last = -1, last_mixed = -1;
+  int wf[4] = {nt, nt, nt, nt}, wl[4] = {-1, -1, -1, -1};  // per-wave first / last visible tile
   for (int t = lane; t < nt; t += 64) {
     const int4 ks = kv_sum[(int64_t)b * nt + t];
     if (classify(q128, ks) == 0) continue;  // not scheduled
@@ -1210,7 +1252,12 @@ __global__ void __launch_bounds__(256) doc_prefix_kernel(const int4* __restrict_
 #pragma unroll
     for (int w4 = 0; w4 < 4; ++w4) {
       if (qs[w4].z + qs[w4].w == 0) continue;  // wave past N
-      if (classify(qs[w4], ks) != 1) last_mixed = t;
+      const int c = classify(qs[w4], ks);
+      if (c != 1) last_mixed = t;
+      if (c != 0) {
+        wf[w4] = min(wf[w4], t);
+        wl[w4] = t;
+      }
     }
   }
 #pragma unroll
@@ -1218,28 +1265,47 @@ __global__ void __launch_bounds__(256) doc_prefix_kernel(const int4* __restrict_
     first = min(first, __shfl_xor(first, off));
     last = max(last, __shfl_xor(last, off));
     last_mixed = max(last_mixed, __shfl_xor(last_mixed, off));
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4) {
+      wf[w4] = min(wf[w4], __shfl_xor(wf[w4], off));
+      wl[w4] = max(wl[w4], __shfl_xor(wl[w4], off));
+    }
   }
-  if (lane == 0) range[item] = make_int4(first, last_mixed + 1, last + 1, 0);
+  bool split = false;
+#pragma unroll
+  for (int w4 = 1; w4 < 4; ++w4)
+    if (qs[w4].z + qs[w4].w != 0 && (wf[w4] != wf[0] || wl[w4] != wl[0])) split = true;
+  if (lane == 0) {
+    int listed = 0;
+    if (split && heavy != nullptr) {
+      const int e = atomicAdd(reinterpret_cast<int*>(heavy), 1);
+      if (e < heavy_max) {
+        heavy[1 + e] = make_int4((int)item, 0, 0, 0);
+        listed = 1;
+      }
+    }
+    range[item] = make_int4(first, last_mixed + 1, last + 1, listed);
+  }
 }
 
 hipError_t launch_doc_prefix(const int4* kv_sum, const int4* q_sum, const int4* q_sum128, int64_t n, int nb,
-                             int4* range, hipStream_t st) {
+                             int4* range, int4* heavy, hipStream_t st) {
   const int nq = (int)(padded_len(n) / 128);
   const int nt = (int)((n + 63) / 64);
   const int64_t waves = (int64_t)nb * nq;
   hipLaunchKernelGGL(doc_prefix_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, kv_sum, q_sum, q_sum128,
-                     nb, nq, nt, range);
+                     nb, nq, nt, range, heavy, kHeavyMax);
   return hipGetLastError();
 }
 
 hipError_t launch_doc_summaries(const int32_t* doc, int64_t n, int nb, int4* kv_sum, int4* q_sum, int4* q_sum128,
-                                hipStream_t st) {
+                                int4* heavy, hipStream_t st) {
   const int64_t np = padded_len(n);
   const int nt = (int)((n + 63) / 64);
   const int64_t total = (int64_t)nb * (nt + np / 32 + np / 128);  // summaries, one wave each
   const int64_t blocks = (total + 3) / 4 < 8192 ? (total + 3) / 4 : 8192;
   hipLaunchKernelGGL(doc_summary_kernel, dim3((unsigned)blocks), dim3(256), 0, st, doc, n, np, nb, nt, kv_sum, q_sum,
-                     q_sum128);
+                     q_sum128, heavy);
   return hipGetLastError();
 }
 
@@ -1247,9 +1313,9 @@ hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, 
                        hipStream_t st) {
   if (mask & 2) {
     hipError_t e = launch_doc_summaries(p.doc, p.n, nb, const_cast<int4*>(p.kv_sum), const_cast<int4*>(p.q_sum),
-                                        const_cast<int4*>(p.q_sum128), st);
+                                        const_cast<int4*>(p.q_sum128), p.heavy, st);
     if (e != hipSuccess) return e;
-    e = launch_doc_prefix(p.kv_sum, p.q_sum, p.q_sum128, p.n, nb, const_cast<int4*>(p.doc_range), st);
+    e = launch_doc_prefix(p.kv_sum, p.q_sum, p.q_sum128, p.n, nb, const_cast<int4*>(p.doc_range), p.heavy, st);
     if (e != hipSuccess) return e;
   }
   if (d == 128) return launch_attn_d<128>(qk, pv, gran, mask, p, st);
@@ -1264,8 +1330,10 @@ AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d) {
   AttnWorkspace w;
   w.split = tail_split(items, nt);
   w.doc_off = 0;
-  // summaries (int4), then the per-query-tile scheduled ranges (int4)
-  w.part_off = ((size_t)(b * (nt + np / 32 + np / 128 + np / 128)) * sizeof(int4) + 255) & ~(size_t)255;
+  // summaries (int4), the per-query-tile scheduled ranges (int4), then the
+  // list of split query tiles (a count and kHeavyMax entries)
+  w.heavy_off = (size_t)(b * (nt + np / 32 + np / 128 + np / 128)) * sizeof(int4);
+  w.part_off = (w.heavy_off + (size_t)(1 + kHeavyMax) * sizeof(int4) + 255) & ~(size_t)255;
   const int64_t pieces = w.split.parts > 1 ? (items - w.split.whole) * w.split.parts : 0;
   w.bytes = w.part_off + (size_t)pieces * (size_t)(128 * d + 512) * sizeof(float);
   return w;

@@ -278,6 +278,8 @@ int attn_fwd_impl(const void* q_codes, const float* q_scale, const void* k_codes
     p.q_sum = p.kv_sum + b * nt;
     p.q_sum128 = p.q_sum + b * (sage::padded_len(n) / 32);
     p.doc_range = p.q_sum128 + b * (sage::padded_len(n) / 128);
+    p.heavy = reinterpret_cast<int4*>(wsp + ws.heavy_off);
+    p.heavy_max = sage::kHeavyMax;
   }
   p.qc = static_cast<const uint8_t*>(q_codes);
   p.qs = q_scale;
@@ -314,7 +316,7 @@ int attn_fwd_impl(const void* q_codes, const float* q_scale, const void* k_codes
     p.split_parts = ws.split.parts;
     p.part = reinterpret_cast<float*>(wsp + ws.part_off);
   }
-  if ((int64_t)p.bh * nq + 8 * sage::kResidentWGs > kMaxGridUnits)
+  if ((int64_t)p.bh * nq + (int64_t)sage::kHeavyMax * h + 8 * sage::kResidentWGs > kMaxGridUnits)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(p.bh * nq));
   p.s_dump = s_dump;
   hipError_t e = sage::launch_attn(qk_kind, pv_kind, granularity, mask, p, d, (int)b, stream);
@@ -477,7 +479,7 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
   const int64_t np = sage::padded_len(n);
   if (doc_ids) {
     e = sage::launch_doc_summaries(doc_ids, n, (int)b, const_cast<int4*>(sums), const_cast<int4*>(sums + b * nkv),
-                                   const_cast<int4*>(sums + b * nkv + b * (np / 32)), stream);
+                                   const_cast<int4*>(sums + b * nkv + b * (np / 32)), nullptr, stream);
     if (e != hipSuccess) return launch_status(e, "sage_attn_bwd (summaries)");
   }
   sage::BwdParams p;

@@ -25,6 +25,11 @@ struct AttnParams {
   // the tile does not see whole (0 if none), one past the last scheduled key
   // tile, 0); an item with no scheduled tile has first = nT, last = 0
   const int4* doc_range;
+  // with document ids: [0].x the number of listed split query tiles, [1 + e].x
+  // = b * nq + qt of entry e < heavy_max (doc_prefix_kernel); the first
+  // heavy_max * h workgroups take them
+  int4* heavy;
+  int heavy_max;
   uint16_t* out;
   // element strides of out per batch, head and row: [B,H,N,D] is
   // (H*N*D, N*D, D), [B,N,H,D] is (N*H*D, D, H*D)
@@ -45,6 +50,10 @@ struct AttnParams {
   // accumulators of every tile the kernel's own loop consumes (row = query)
   int32_t* s_dump;
 };
+
+// Split query tiles (document ids) that the first workgroups of a launch take
+// (AttnParams::heavy): kHeavyMax * h workgroups are reserved for them.
+constexpr int kHeavyMax = 2;
 
 // Resident workgroups of the attention kernel on MI355X: 256 CUs x 2.
 constexpr int kResidentWGs = 512;
@@ -133,14 +142,17 @@ hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, 
 // The scheduled key-tile range of each 128-row query tile and one past the
 // last key tile that some live wave of it does not see whole (the doc_range
 // entries), from the summaries (after launch_doc_summaries).
+// Also lists the query tiles whose live waves see different key-tile ranges
+// (heavy, when not null; see AttnParams::heavy).
 hipError_t launch_doc_prefix(const int4* kv_sum, const int4* q_sum, const int4* q_sum128, int64_t n, int nb,
-                             int4* range, hipStream_t st);
+                             int4* range, int4* heavy, hipStream_t st);
+// heavy (may be null): the split-query-tile list to empty before launch_doc_prefix.
 hipError_t launch_doc_summaries(const int32_t* doc, int64_t n, int nb, int4* kv_sum, int4* q_sum, int4* q_sum128,
-                                hipStream_t st);
+                                int4* heavy, hipStream_t st);
 // Workspace of one attention call: the doc-id summaries, then the partial
 // slots of the tail split.
 struct AttnWorkspace {
-  size_t doc_off, part_off, bytes;
+  size_t doc_off, heavy_off, part_off, bytes;
   TailSplit split;
 };
 AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d);

@@ -62,6 +62,7 @@ def test_sizes_and_padding():
     assert lib.sage_quant_workspace_bytes(1, 20000, 64) == 40 * (64 + 1) * 8
     # per-batch summaries of every 64-key tile and 32- and 128-row query block
     # and the scheduled key-tile range of each 128-row query block (int4 each),
+    # the list of split query tiles (a count and 2 entries, int4 each),
     # then (256-byte aligned) fp32 slots of 128 x D + 512 floats for the pieces
     # of the split tail: 26 items x 4 pieces (the cap) at the 1x30x4416x128
     # headline shape (1050 items = 2 rounds of 512 + 26); below one round,
@@ -71,7 +72,7 @@ def test_sizes_and_padding():
                                (1, 30, 1280, 128, 44 * 2), (1, 40, 1280, 128, 0), (1, 26, 1280, 128, 4 * 2),
                                (2, 30, 4416, 128, 52 * 4)):
         np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
-        doc = (b * (nt + np_ // 32 + 2 * (np_ // 128)) * 16 + 255) // 256 * 256
+        doc = ((b * (nt + np_ // 32 + 2 * (np_ // 128)) + 1 + 2) * 16 + 255) // 256 * 256
         assert lib.sage_attn_workspace_bytes(b, h, n, d) == doc + pieces * (128 * d + 512) * 4
 
 
