@@ -10,6 +10,7 @@ libsage_probe.so.
 
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -56,16 +57,21 @@ def build(verbose: bool = False) -> str:
     returns LIB_PATH."""
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="sage_build_") as tmp:
-        objs = []
-        for src in SOURCES + [PROBE_SOURCE]:
-            obj = os.path.join(tmp, src + ".o")
-            cmd = [cc, *flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+        srcs = SOURCES + [PROBE_SOURCE]
+        objs = [os.path.join(tmp, src + ".o") for src in srcs]
+
+        def compile_one(i: int) -> None:
+            cmd = [cc, *flags(), "-c", os.path.join(CSRC, srcs[i]), "-o", objs[i]]
             if verbose:
                 print(" ".join(cmd), flush=True)
             res = subprocess.run(cmd, capture_output=True, text=True)
             if res.returncode != 0:
-                raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
-            objs.append(obj)
+                raise RuntimeError(f"hipcc failed on {srcs[i]}:\n{res.stderr}")
+
+        # one hipcc process per source file, at most four at a time
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(4, len(srcs))) as pool:
+            for f in [pool.submit(compile_one, i) for i in range(len(srcs))]:
+                f.result()
         _link(cc, objs[:-1], tmp, LIB_PATH)
         _link(cc, objs[-1:], tmp, PROBE_LIB_PATH)
     return LIB_PATH
