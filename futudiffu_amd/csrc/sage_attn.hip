@@ -450,21 +450,43 @@ __device__ __forceinline__ void softmax_fp8(float (&u)[2][16], float wt, float& 
 // lanes h = b, with A = rsc of query r (lane-local in the S^T layout) and B =
 // the V scale of channel 32(c2 + b) + r; each product is one correctly
 // rounded fp32 multiply, as on the vector ALU, and no lane exchange is needed.
+// The stage operands of one chunk pair's fp8 P.V: the V fragments of chunks
+// c2 and c2 + 1 and the V scale this lane feeds the factor MFMA.
+struct PvFrags {
+  i32x4 v[4];
+  float vd;
+};
+
 template <int D>
-__device__ __forceinline__ void pv_issue(const uint8_t* sb, const i32x8& pa, float rsc, int lane, int c2, f32x16& p0,
-                                         f32x16& p1, f32x32& rv) {
+__device__ __forceinline__ PvFrags pv_load(const uint8_t* sb, int lane, int c2) {
   using St = Stage<D, kPV_FP8>;
   const int h = lane >> 5, r = lane & 31;
   const i32x4* vl = reinterpret_cast<const i32x4*>(sb + St::offV);
   const float* vdl = reinterpret_cast<const float*>(sb + St::offVd);
-  rv = __builtin_amdgcn_mfma_f32_32x32x1f32(rsc, vdl[32 * (c2 + h) + r], f32x32{0}, 0, 0, 0);
-  auto pv = [&](int c) {
-    const i32x4 b0 = vl[(c * 2 + 0) * 64 + lane], b1 = vl[(c * 2 + 1) * 64 + lane];
+  PvFrags f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f.v[i] = vl[(c2 * 2 + i) * 64 + lane];
+  f.vd = vdl[32 * (c2 + h) + r];
+  return f;
+}
+
+template <int D>
+__device__ __forceinline__ void pv_issue_f(const PvFrags& f, const i32x8& pa, float rsc, f32x16& p0, f32x16& p1,
+                                           f32x32& rv) {
+  rv = __builtin_amdgcn_mfma_f32_32x32x1f32(rsc, f.vd, f32x32{0}, 0, 0, 0);
+  auto pv = [&](int i) {
+    const i32x4 b0 = f.v[2 * i], b1 = f.v[2 * i + 1];
     const i32x8 bv = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(pa, bv, f32x16{0}, 0, 0, 0, 0, 0, 0);
   };
-  p0 = pv(c2);
-  p1 = pv(c2 + 1);
+  p0 = pv(0);
+  p1 = pv(1);
+}
+
+template <int D>
+__device__ __forceinline__ void pv_issue(const uint8_t* sb, const i32x8& pa, float rsc, int lane, int c2, f32x16& p0,
+                                         f32x16& p1, f32x32& rv) {
+  pv_issue_f<D>(pv_load<D>(sb, lane, c2), pa, rsc, p0, p1, rv);
 }
 
 __device__ __forceinline__ void pv_accum(f32x16* o, int c2, const f32x16& p0, const f32x16& p1, const f32x32& rv) {
@@ -851,6 +873,13 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     float alpha_p = 1.0f;
     bool move_p = false;
     int stage_p = 0;
+    // fp8: the first chunk pair's stage operands of the pending product, read
+    // at the end of the iteration that forms its P codes (before the barrier,
+    // whose wait covers their LDS latency)
+    PvFrags pf0;
+    auto prefetch_pending = [&]() __attribute__((always_inline)) {
+      if constexpr (PV == kPV_FP8) pf0 = pv_load<D>(sp(stage), lane, 0);
+    };
     float u[2][16];
     auto softmax_p = [&]() __attribute__((always_inline)) {
       if constexpr (PV == kPV_FP8)
@@ -884,6 +913,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
       if (t1 < t_end) qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
       softmax_p();
       stage_p = stage;
+      prefetch_pending();
       publish();
       advance();
     }
@@ -901,7 +931,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
       if constexpr (PV == kPV_FP8) {
         f32x16 p0, p1;
         f32x32 rv;
-        pv_issue<D>(sbp, pa_p, rsc_p, lane, 0, p0, p1, rv);
+        pv_issue_f<D>(pf0, pa_p, rsc_p, p0, p1, rv);
         scores(0, u[0]);
         if constexpr (NP == 1) scores(1, u[1]);
         pv_accum(o, 0, p0, p1, rv);
@@ -939,6 +969,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
         softmax_p();
       }
       stage_p = stage;
+      prefetch_pending();
       publish();
       advance();
     };
