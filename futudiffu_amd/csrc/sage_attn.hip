@@ -874,11 +874,12 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     bool move_p = false;
     int stage_p = 0;
     // fp8: the first chunk pair's stage operands of the pending product, read
-    // at the end of the iteration that forms its P codes (before the barrier,
-    // whose wait covers their LDS latency)
+    // in the iteration that forms its P codes, before its softmax, whose
+    // vector work covers their LDS latency (the barrier waits for every LDS
+    // access in flight)
     PvFrags pf0;
     auto prefetch_pending = [&]() __attribute__((always_inline)) {
-      if constexpr (PV == kPV_FP8) pf0 = pv_load<D>(sp(stage), lane, 0);
+      if constexpr (PV == kPV_FP8) pf0 = pv_load<D>(sp(stage), lane, 0);  // the tile about to become pending
     };
     float u[2][16];
     auto softmax_p = [&]() __attribute__((always_inline)) {
@@ -911,9 +912,9 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
       half_scores<D, QK, PV, GRAN, false>(sp(stage), s0, 0, h, kdb, kvalid, false, dq, u[0]);
       half_scores<D, QK, PV, GRAN, false>(sp(stage), s1, 1, h, kdb, kvalid, false, dq, u[1]);
       if (t1 < t_end) qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
+      prefetch_pending();
       softmax_p();
       stage_p = stage;
-      prefetch_pending();
       publish();
       advance();
     }
@@ -958,6 +959,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
         // fp8/fp8: 234.7 -> 230.7 us and 240.3 -> 235.7 us; with int8 QK the
         // same order measured 247.7 -> 250.8 us: the other wave of the SIMD
         // already covers the QK^T burst)
+        prefetch_pending();
         const float bm = row_max_move<D>(u, w, m_ref, l_acc, o, xrow, h, r);
         softmax_fp8_exp_qk<D>(u, w, bm, m_ref, l_acc, pa_p, rsc_p, sp(next_stage(stage, 1)), qf, lane, s0, s1);
       } else {
@@ -966,10 +968,10 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
           if constexpr (QK != kQK_INT8) pv_bf16_pair<D>(sbp, pb_p, lane, 0, o);
           if constexpr (NP == 2) pv_bf16_pair<D>(sbp, pb_p, lane, 2, o);
         }
+        prefetch_pending();
         softmax_p();
       }
       stage_p = stage;
-      prefetch_pending();
       publish();
       advance();
     };
