@@ -58,15 +58,14 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sdpa", action="store_true",
+                    help="--all-configs: skip the GPU scaled_dot_product_attention line of the unmasked cases")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device copy of MIB MiB "
                          "--steps times (scales the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--stream-calibration", action="store_true",
                     help="instead of the benchmark, time a 2:1 read/write stream at the quantization's "
                          "traffic and at 1 GiB, warm and cold")
-    ap.add_argument("--isa-probe", action="store_true",
-                    help="instead of the benchmark, measure gfx950 issue costs and MFMA/VALU co-execution "
-                         "with the probes of futudiffu_amd/libsage_probe.so")
     ap.add_argument("--all-configs", action="store_true",
                     help="one JSON line per benchmark configuration instead of the headline line")
     ap.add_argument("--cases", default="",
@@ -274,6 +273,44 @@ def prewarm(step, seconds):
             return {"seconds": round(time.perf_counter() - t0, 4), "steps": n}
 
 
+def sdpa_gpu(qd, kd, vd, sm, args):
+    """torch's scaled_dot_product_attention on the same bf16 q, k, v on the
+    GPU, the comparison the reference publishes for its Sage op
+    (bench/bench_attention.py:57-58): median over --steps calls between HIP
+    events, after the same pre-warm and warm-up.  Only the fused backends
+    (flash, then memory-efficient) are allowed: the unfused math path forms
+    the N x N scores with batched bf16 products of a transposed operand.
+    Context for the comparison, not part of the measured op."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    B, H, N, D = qd.shape
+    flop = 4.0 * B * H * N * N * D
+    for name, backend in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([backend]):
+                def call():
+                    F.scaled_dot_product_attention(qd, kd, vd, scale=sm)
+                call()
+                torch.cuda.synchronize()
+                prewarm(call, args.prewarm_seconds)
+                for _ in range(args.warmup):
+                    call()
+                evs = [(TimingEvent(), TimingEvent()) for _ in range(args.steps)]
+                for e in evs:
+                    e[0].record()
+                    call()
+                    e[1].record()
+                torch.cuda.synchronize()
+        except RuntimeError as err:
+            last = f"{name}: {str(err).splitlines()[0][:160]}"
+            continue
+        ms = sorted(e[0].elapsed_time(e[1]) for e in evs)[len(evs) // 2]
+        tf = flop / (ms * 1e-3) / 1e12
+        return {"backend": name, "dtype": "bf16", "ms": round(ms, 5), "tflops": round(tf, 2),
+                "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    return {"unavailable": last}
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -334,42 +371,6 @@ def stream_calibration(args):
         for cold in (False, True):
             out[f"{label}_{'cold' if cold else 'warm'}_GBs"] = round(stream_rate(nbytes, cold), 1)
     print(json.dumps(out), flush=True)
-
-
-def isa_probe(args):
-    """Issue cost per wave-instruction (s_memtime ticks = shader clock) at one
-    and two waves per SIMD, and the co-execution of MFMA and FMA streams on
-    one SIMD, from libsage_probe.so (csrc/sage_probe.hip)."""
-    import ctypes
-    torch.cuda.init()
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "futudiffu_amd", "libsage_probe.so")
-    lib = ctypes.CDLL(path)
-    for fn in ("sage_probe_last_error", "sage_probe_issue_name", "sage_probe_coexec_variant", "sage_probe_coexec_mode"):
-        getattr(lib, fn).restype = ctypes.c_char_p
-    lib.sage_probe_issue_name.argtypes = [ctypes.c_int]
-    lib.sage_probe_coexec_variant.argtypes = [ctypes.c_int]
-    lib.sage_probe_coexec_mode.argtypes = [ctypes.c_int]
-    for fn in ("sage_probe_issue", "sage_probe_coexec"):
-        getattr(lib, fn).argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.c_int]
-    ni = lib.sage_probe_issue_count()
-    buf = (ctypes.c_double * (2 * ni))()
-    if lib.sage_probe_issue(buf, 2 * ni) < 0:
-        raise RuntimeError(lib.sage_probe_last_error().decode())
-    issue = {lib.sage_probe_issue_name(i).decode(): {"1_wave_per_simd": round(buf[2 * i], 2),
-                                                     "2_waves_per_simd": round(buf[2 * i + 1], 2)}
-             for i in range(ni)}
-    nc = lib.sage_probe_coexec_count()
-    cbuf = (ctypes.c_double * (2 * nc))()
-    if lib.sage_probe_coexec(cbuf, 2 * nc) < 0:
-        raise RuntimeError(lib.sage_probe_last_error().decode())
-    coexec = [{"variant": lib.sage_probe_coexec_variant(i).decode(), "mode": lib.sage_probe_coexec_mode(i).decode(),
-               "waves_0_3_ticks_per_iter": round(cbuf[2 * i], 1), "waves_4_7_ticks_per_iter": round(cbuf[2 * i + 1], 1)}
-              for i in range(nc)]
-    print(json.dumps({"isa_probe": "gfx950", "unit": "s_memtime ticks (shader clock)",
-                      "issue_ticks_per_wave_instruction": issue,
-                      "coexec_note": "per iteration: 4 MFMA pairs and 4x the FMA count per pair; waves w and w+4 "
-                                     "share SIMD w",
-                      "coexec": coexec}), flush=True)
 
 
 def _case_inputs(c, dev, seed=0):
@@ -666,6 +667,11 @@ def all_configs(args):
         if c["pv"] == "bf16" and c["qk"] == "fp8":
             line["roofline"]["frac_of_mixed_fp8_bf16_peak"] = round(tf / PEAK_MIXED_TFLOPS, 4)
         line.update(extra)
+        if not args.no_sdpa and bm is None and doc is None and not c.get("producer") and layout == "bhnd":
+            s = sdpa_gpu(qd, kd, vd, sm, args)
+            if "ms" in s:
+                s["sage_op_speedup"] = round(s["ms"] / (a_ms + q_ms), 3)
+            line["sdpa_gpu_same_inputs"] = s
         if not args.no_cpu_baseline:
             line["cpu_baseline"] = _cpu_case(c, q, k, v, bm, doc, flop, args.cpu_seconds)
         print(json.dumps(line), flush=True)
@@ -682,9 +688,6 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args)
-        return
-    if args.isa_probe:
-        isa_probe(args)
         return
     if args.stream_calibration:
         stream_calibration(args)

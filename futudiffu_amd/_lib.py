@@ -26,6 +26,7 @@ SIGNATURES = {
         _P, _P, _P, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_float,
         _P, _P, _P, _P, _P, _P, _P, _P, _c.c_size_t, _P]),
     "sage_attn_workspace_bytes": (_c.c_size_t, [_I64, _I64, _I64, _I64]),
+    "sage_attn_masked_workspace_bytes": (_c.c_size_t, [_I64, _I64, _I64, _I64]),
     "sage_attn_fwd": (_c.c_int, [
         _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_int,
         _P, _I64, _I64, _I64, _P, _P, _c.c_size_t, _P, _c.c_int, _P, _P]),
@@ -33,7 +34,7 @@ SIGNATURES = {
         _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _c.c_int,
         _P, _I64, _I64, _I64, _P, _P, _c.c_int, _P, _P]),
     "sage_attn_qk_accumulators": (_c.c_int, [
-        _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _P, _c.c_size_t, _P, _P, _P, _P]),
+        _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_int, _c.c_int, _P, _c.c_size_t, _P, _P, _P, _P]),
     "sage_build_tile_mask": (_c.c_int, [_P, _I64, _I64, _c.c_int32, _P, _P]),
     "sage_qkv_postprocess": (_c.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _c.c_float, _P, _P, _P, _P]),
     "sage_qkv_postprocess_bwd": (_c.c_int, [

@@ -3,9 +3,7 @@
 Compiles the HIP sources under ``csrc/`` with ``hipcc`` into one in-tree
 shared library.  Packed fp32 VALU instructions are disabled
 (``-packed-fp32-ops``); no fast-math flags are used, so fp32 division stays
-correctly rounded, which the quantization codes depend on.  The issue-cost
-probes behind ``bench.py --isa-probe`` go into a library of their own,
-libsage_probe.so.
+correctly rounded, which the quantization codes depend on.
 """
 
 from __future__ import annotations
@@ -22,8 +20,6 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libsage_mi355x.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 SOURCES = ["sage_quant.hip", "sage_attn.hip", "sage_mask.hip", "sage_bwd.hip", "sage_capi.hip"]
-PROBE_SOURCE = "sage_probe.hip"
-PROBE_LIB_PATH = os.path.join(HERE, "libsage_probe.so")
 ARCH = "gfx950"
 
 
@@ -53,11 +49,10 @@ def _link(cc: str, objs: list[str], tmp: str, path: str) -> None:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every source and link LIB_PATH (and PROBE_LIB_PATH) atomically;
-    returns LIB_PATH."""
+    """Compile every source and link LIB_PATH atomically; returns LIB_PATH."""
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="sage_build_") as tmp:
-        srcs = SOURCES + [PROBE_SOURCE]
+        srcs = SOURCES
         objs = [os.path.join(tmp, src + ".o") for src in srcs]
 
         def compile_one(i: int) -> None:
@@ -72,8 +67,7 @@ def build(verbose: bool = False) -> str:
         with concurrent.futures.ThreadPoolExecutor(max_workers=min(4, len(srcs))) as pool:
             for f in [pool.submit(compile_one, i) for i in range(len(srcs))]:
                 f.result()
-        _link(cc, objs[:-1], tmp, LIB_PATH)
-        _link(cc, objs[-1:], tmp, PROBE_LIB_PATH)
+        _link(cc, objs, tmp, LIB_PATH)
     return LIB_PATH
 
 

@@ -590,7 +590,7 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
 // leaves the wave's O, reference point and row-sum half in o / m_ref / l_acc
 // (O and l in the frame of m_ref; all zero / -inf for a wave past N).
 // Ends with a workgroup barrier, after which the stage ring may be reused.
-// DUMP (int8 QK only) also stores every S^T accumulator pair this loop
+// DUMP (per-token scales) also stores every S^T accumulator pair this loop
 // consumes into p.s_dump, at the point where it is consumed.
 template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false>
 __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, int bh, int qt, int t_begin,
@@ -672,8 +672,11 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
   const __amdgpu_buffer_rsrc_t rs_ks = raw_rsrc(p.ks + (int64_t)bh * p.np, (uint32_t)(p.np * 4));
   const __amdgpu_buffer_rsrc_t rs_vs =
       raw_rsrc(PV == kPV_FP8 ? p.vs + (int64_t)bh * (p.np / 64) * D : p.ks, (uint32_t)(p.np / 64 * D * 4));
-  // document ids of the keys, copied like the scales (fp8 P.V): ids past N
-  // read as 0, which no score sees, since keys past N are masked by count
+  // document ids of the keys, copied like the scales (fp8 P.V).  The whole
+  // offset goes in the vector operand, the part the buffer range check
+  // covers (per dword for a 16-byte load), so ids past N read as 0 and no
+  // byte past the caller's [B, N] array is fetched; no score sees those ids,
+  // since keys past N are masked by count
   constexpr bool kDocDma = (MASK & 2) && PV == kPV_FP8;
   const __amdgpu_buffer_rsrc_t rs_doc =
       raw_rsrc(kDocDma ? static_cast<const void*>(docb) : static_cast<const void*>(p.ks), (uint32_t)(p.n * 4));
@@ -692,7 +695,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_vs, sbw + St::offKd, 16, (lane - 16) * 16, tt * D * 4, 0, 0);
     }
     if (kDocDma && wave_u == 1 && lane < 16)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_doc, sbw + St::offDoc, 16, lane * 16, tt * 256, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_doc, sbw + St::offDoc, 16, tt * 256 + lane * 16, 0, 0, 0);
     if (!kDocDma && (MASK & 2) && tid >= 48 && tid < 64) {
       const int64_t base = (int64_t)tt * 64 + (tid - 48) * 4;
       pre_doc.x = base + 0 < p.n ? docb[base + 0] : -1;
@@ -715,15 +718,20 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
   // the S^T accumulators of tile tt (keys 64 tt + 32 b + 8 j + 4 h + i of
   // query q0 + r) as the loop consumes them; only live waves call it, so
   // q0 + r < Np, and every key index is below 64 nt <= Np
+  // (int32 for int8 QK, the bit patterns of the fp32 sums for fp8 QK)
   auto dump = [&](int tt, const SAcc& a0, const SAcc& a1) __attribute__((always_inline)) {
-    if constexpr (DUMP && QK == kQK_INT8) {
+    if constexpr (DUMP) {
       int32_t* row = p.s_dump + ((int64_t)bh * p.np + q0 + r) * p.np + (int64_t)tt * 64 + 4 * h;
+      auto word = [](auto x) -> int32_t {
+        if constexpr (QK == kQK_INT8) return x;
+        else return __float_as_int(x);
+      };
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          row[8 * j + i] = a0[4 * j + i];
-          row[32 + 8 * j + i] = a1[4 * j + i];
+          row[8 * j + i] = word(a0[4 * j + i]);
+          row[32 + 8 * j + i] = word(a1[4 * j + i]);
         }
     }
   };
@@ -1220,8 +1228,8 @@ hipError_t launch_attn_g(int mask, const AttnParams& p, hipStream_t st) {
   // with document ids the first heavy_max * h workgroups take the listed split query tiles
   const dim3 grid((unsigned)(mask == 0 ? p.n_whole + n_split * p.split_parts
                                        : items + ((mask & 2) ? (int64_t)p.heavy_max * p.h : 0)));
-  // the accumulator dump exists for the int8 QK, per-token, unmasked kernels
-  constexpr bool kDumpable = QK == kQK_INT8 && GRAN == kGRAN_TOKEN;
+  // the accumulator dump exists for the per-token, unmasked kernels
+  constexpr bool kDumpable = GRAN == kGRAN_TOKEN;
   if (p.s_dump != nullptr) {
     if (!kDumpable || mask != 0) return hipErrorInvalidValue;
     if constexpr (kDumpable) hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 0, true>), grid, dim3(256), 0, st, p);
@@ -1356,7 +1364,7 @@ hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, 
   return hipErrorInvalidValue;
 }
 
-AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d) {
+AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d, bool masked) {
   const int64_t np = padded_len(n);
   const int64_t nt = (n + 63) / 64;
   const int64_t items = b * h * (np / kRowsPerWG);
@@ -1367,11 +1375,13 @@ AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d) {
   // list of split query tiles (a count and kHeavyMax entries)
   w.heavy_off = (size_t)(b * (nt + np / 32 + np / 128 + np / 128)) * sizeof(int4);
   w.part_off = (w.heavy_off + (size_t)(1 + kHeavyMax) * sizeof(int4) + 255) & ~(size_t)255;
-  const int64_t pieces = w.split.parts > 1 ? (items - w.split.whole) * w.split.parts : 0;
+  const int64_t pieces = !masked && w.split.parts > 1 ? (items - w.split.whole) * w.split.parts : 0;
   w.bytes = w.part_off + (size_t)pieces * (size_t)(128 * d + 512) * sizeof(float);
   return w;
 }
 
-size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) { return attn_workspace(b, h, n, d).bytes; }
+size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d, bool masked) {
+  return attn_workspace(b, h, n, d, masked).bytes;
+}
 
 }  // namespace sage

@@ -63,6 +63,10 @@ size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) {
   return sage::attn_workspace_bytes(b, h, n, d);
 }
 
+size_t sage_attn_masked_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d) {
+  return sage::attn_workspace_bytes(b, h, n, d, true);
+}
+
 }  // extern "C"
 
 namespace {
@@ -264,15 +268,16 @@ int attn_fwd_impl(const void* q_codes, const float* q_scale, const void* k_codes
       return fail(SAGE_ERR_ARG, "mask_stride_z must be 0 (2D mask) or %lld (3D mask)", (long long)(nq * nkv));
     mask |= 1;
   }
+  if (doc_ids) mask |= 2;
   sage::AttnParams p;
   memset(&p, 0, sizeof(p));
-  const sage::AttnWorkspace ws = sage::attn_workspace(b, h, n, d);
+  // masked launches cut no item, so they need no partial slots
+  const sage::AttnWorkspace ws = sage::attn_workspace(b, h, n, d, mask != 0);
   if (!workspace || workspace_bytes < ws.bytes)
     return fail(SAGE_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", ws.bytes, workspace_bytes);
   if (!aligned16(workspace)) return fail(SAGE_ERR_ALIGN, "workspace must be 16-byte aligned");
   uint8_t* wsp = static_cast<uint8_t*>(workspace);
   if (doc_ids) {
-    mask |= 2;
     const int64_t nt = nkv;
     p.kv_sum = reinterpret_cast<const int4*>(wsp + ws.doc_off);
     p.q_sum = p.kv_sum + b * nt;
@@ -385,7 +390,7 @@ int sage_attn_fwd_noalloc(const void* q_codes, const float* q_scale, const void*
   if (b <= 0 || h <= 0) return fail(SAGE_ERR_ARG, "b=%lld and h=%lld must be positive", (long long)b, (long long)h);
   int st = check_common(b * h, n, d, qk_kind, pv_kind, granularity);
   if (st) return st;
-  const size_t need = sage::attn_workspace_bytes(b, h, n, d);
+  const size_t need = sage::attn_workspace_bytes(b, h, n, d, tile_mask != nullptr || doc_ids != nullptr);
   if (need > (size_t)SAGE_NOALLOC_SCRATCH_BYTES)
     return fail(SAGE_ERR_WORKSPACE,
                 "b=%lld h=%lld n=%lld d=%lld needs %zu bytes of workspace, beyond the %zu-byte scratch of the "
@@ -401,10 +406,10 @@ int sage_attn_fwd_noalloc(const void* q_codes, const float* q_scale, const void*
 
 int sage_attn_qk_accumulators(const void* q_codes, const float* q_scale, const void* k_codes, const float* k_scale,
                               const void* v_in, const float* v_scale, int64_t b, int64_t h, int64_t n, int64_t d,
-                              int pv_kind, void* workspace, size_t workspace_bytes, void* out, float* lse,
+                              int qk_kind, int pv_kind, void* workspace, size_t workspace_bytes, void* out, float* lse,
                               int32_t* s_out, hipStream_t stream) {
   if (!s_out) return fail(SAGE_ERR_ARG, "null tensor pointer");
-  return attn_fwd_impl(q_codes, q_scale, k_codes, k_scale, v_in, v_scale, b, h, n, d, SAGE_QK_INT8, pv_kind,
+  return attn_fwd_impl(q_codes, q_scale, k_codes, k_scale, v_in, v_scale, b, h, n, d, qk_kind, pv_kind,
                        SAGE_GRAN_TOKEN, nullptr, 0, 0, 0, nullptr, workspace, workspace_bytes, out, SAGE_OUT_BHND,
                        lse, s_out, "sage_attn_qk_accumulators", stream);
 }

@@ -155,8 +155,10 @@ struct AttnWorkspace {
   size_t doc_off, heavy_off, part_off, bytes;
   TailSplit split;
 };
-AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d);
-size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
+// `masked`: a launch with a tile mask or document ids, which splits no item
+// and so needs no partial slots
+AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d, bool masked = false);
+size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d, bool masked = false);
 hipError_t launch_tile_mask(const int32_t* doc, int64_t nb, int64_t n, int32_t pad_fill, uint8_t* mask,
                             hipStream_t st);
 

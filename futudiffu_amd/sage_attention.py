@@ -281,7 +281,10 @@ def attn_from_quantized(qz: SageQuantized, B: int, H: int, *, block_mask: Tensor
         if doc_ids.shape != (B, N):
             raise ValueError(f"doc_ids must be [B, N] = [{B}, {N}], got {tuple(doc_ids.shape)}")
         doc_ids = doc_ids.to(device=dev, dtype=torch.int32).contiguous()
-    wsb = int(lib.sage_attn_workspace_bytes(B, H, N, D))
+    if bm is None and doc_ids is None:
+        wsb = int(lib.sage_attn_workspace_bytes(B, H, N, D))
+    else:
+        wsb = int(lib.sage_attn_masked_workspace_bytes(B, H, N, D))
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     if out is None:
         out = torch.empty(out_shape, dtype=torch.bfloat16, device=dev)
@@ -447,18 +450,17 @@ def sage_attn_backward_masked(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse:
 
 
 def qk_accumulators(qz: SageQuantized, B: int, H: int) -> tuple[Tensor, Tensor, Tensor]:
-    """The attention forward (int8 QK, per-token scales, no mask) on quantized
-    operands, plus the int32 QK^T accumulators its own loop formed.
+    """The attention forward (per-token scales, no mask) on quantized
+    operands, plus the QK^T accumulators its own loop formed.
 
-    Returns ``(out, lse, s)`` with ``s`` int32 ``[B*H, Np, Np]`` (row = query,
-    column = key): the result of ``tl.dot(q_int8, k_int8)``
-    (sage_kernels.py:1451) as the kernel's pipelined loop consumed it, tile
-    by tile.  Entries past ``32*ceil(N/32)`` rows or ``64*ceil(N/64)`` keys
-    stay zero.  Codes quantized with per-64-token scales run with those
-    scales repeated per token (the accumulators depend on the codes only).
+    Returns ``(out, lse, s)`` with ``s`` ``[B*H, Np, Np]`` (row = query,
+    column = key): the result of ``tl.dot(q, k)`` before dequantization
+    (int8 sage_kernels.py:1451, int32; fp8 :282, float32) as the kernel's
+    pipelined loop consumed it, tile by tile.  Entries past ``32*ceil(N/32)``
+    rows or ``64*ceil(N/64)`` keys stay zero.  Codes quantized with
+    per-64-token scales run with those scales repeated per token (the
+    accumulators depend on the codes only).
     """
-    if qz.qk != "int8":
-        raise ValueError("the accumulator dump covers int8 QK")
     lib = _lib.load()
     BH, N, D = B * H, qz.n, qz.d
     dev = qz.q_codes.device
@@ -472,9 +474,9 @@ def qk_accumulators(qz: SageQuantized, B: int, H: int) -> tuple[Tensor, Tensor, 
     s = torch.zeros(BH, qz.np_, qz.np_, dtype=torch.int32, device=dev)
     _lib.check(lib.sage_attn_qk_accumulators(
         qz.q_codes.data_ptr(), qs.data_ptr(), qz.k_codes.data_ptr(), ks.data_ptr(),
-        qz.v_op.data_ptr(), _ptr(qz.v_scale), B, H, N, D, _PV[qz.pv], ws.data_ptr(), wsb, out.data_ptr(),
-        lse.data_ptr(), s.data_ptr(), _stream_handle(dev)))
-    return out, lse, s
+        qz.v_op.data_ptr(), _ptr(qz.v_scale), B, H, N, D, _QK[qz.qk], _PV[qz.pv], ws.data_ptr(), wsb,
+        out.data_ptr(), lse.data_ptr(), s.data_ptr(), _stream_handle(dev)))
+    return out, lse, (s if qz.qk == "int8" else s.view(torch.float32))
 
 
 # ---- legacy ops (sage_attention.py:664-690, :740-769) ----------------------------------

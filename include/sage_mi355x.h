@@ -170,9 +170,15 @@ int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* 
  * key-tile range of every 128-row query block (written and used when doc_ids
  * is given), then the fp32 partial results of the key-tile pieces of
  * the 128-row items that an unmasked launch splits (the items past the last
- * whole round of 512 resident workgroups).  No reference counterpart (the
- * Triton launch needs no workspace). */
+ * whole round of 512 resident workgroups).  Enough for every launch of that
+ * shape.  No reference counterpart (the Triton launch needs no workspace). */
 size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
+
+/* Bytes of device workspace a sage_attn_fwd launch with a tile_mask or
+ * doc_ids needs: the summaries only, since masked launches split no item
+ * (a few KB; 7 KB for the packed 1x30x6912 batch).  No reference
+ * counterpart. */
+size_t sage_attn_masked_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
 
 /* Fused attention forward over pre-quantized operands.
  * Replaces the launch of _sage_attn_fwd_int8qk_bf16pv_masked_lse
@@ -195,8 +201,9 @@ size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
  *                 32-bit byte offsets).
  *   h             heads per batch (row z of q belongs to batch z / h).
  *   workspace     device memory of sage_attn_workspace_bytes(b, h, n, d)
- *                 bytes, 16-byte aligned.  Concurrent calls need separate
- *                 workspaces.
+ *                 bytes (sage_attn_masked_workspace_bytes when tile_mask or
+ *                 doc_ids is given), 16-byte aligned.  Concurrent calls need
+ *                 separate workspaces.
  *   out_layout    SAGE_OUT_BHND (the reference op's output) or SAGE_OUT_BNHD
  *                 (fuses JointAttention's out.transpose(1, 2).reshape(b, -1,
  *                 H*D), transformer.py:471).  Values are bit-identical
@@ -220,9 +227,12 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale,
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
  * workspace lives in a fixed device array of SAGE_NOALLOC_SCRATCH_BYTES per
- * GPU, held until the process ends; shapes whose sage_attn_workspace_bytes
- * exceed it are rejected with SAGE_ERR_WORKSPACE before any launch (the
- * 1x30x4416x128 headline needs 6.9 MB).  The call allocates and frees
+ * GPU, held until the process ends; launches whose workspace (as
+ * sage_attn_fwd: sage_attn_workspace_bytes unmasked,
+ * sage_attn_masked_workspace_bytes with a tile mask or document ids) exceeds
+ * it are rejected with SAGE_ERR_WORKSPACE before any launch (the unmasked
+ * 1x30x4416x128 headline needs 6.9 MB, the masked packed 1x30x6912 batch
+ * 7 KB).  The call allocates and frees
  * nothing and needs no memory cleared beforehand: every byte of scratch it
  * reads was written earlier in the same call.  Every call on one GPU shares
  * that GPU's scratch, so calls that overlap on one GPU (other streams, other
@@ -309,19 +319,21 @@ int sage_attn_bwd(const void* q, const void* k, const void* v,
                   void* dq, void* dk, void* dv,
                   hipStream_t stream);
 
-/* Parity: sage_attn_fwd with int8 QK, per-token scales, no mask and the
- * [B, H, N, D] output, which also stores the int32 QK^T accumulators its own
- * loop consumes, tile by tile, as that loop forms them (the split tail pieces
- * included): s_out int32 [B*H, Np, Np], row = query, column = key; entries of
- * rows below 32*ceil(n/32) and keys below 64*ceil(n/64) are written, others
- * are left as they were.  Exposes the int32 result of tl.dot(q_int8, k_int8)
- * (sage_kernels.py:1451).  Other arguments as sage_attn_fwd; slower (the
- * accumulators are stored from inside the loop). */
+/* Parity: sage_attn_fwd with per-token scales, no mask and the [B, H, N, D]
+ * output, which also stores the QK^T accumulators its own loop consumes, tile
+ * by tile, as that loop forms them (the split tail pieces included): s_out
+ * [B*H, Np, Np] 32-bit words, row = query, column = key; int32 sums for
+ * SAGE_QK_INT8, the bit patterns of the fp32 sums for SAGE_QK_FP8.  Entries
+ * of rows below 32*ceil(n/32) and keys below 64*ceil(n/64) are written,
+ * others are left as they were.  Exposes the result of tl.dot(q, k) before
+ * dequantization (int8 sage_kernels.py:1451, fp8 :282).  Other arguments as
+ * sage_attn_fwd; slower (the accumulators are stored from inside the
+ * loop). */
 int sage_attn_qk_accumulators(const void* q_codes, const float* q_scale,
                               const void* k_codes, const float* k_scale,
                               const void* v_in, const float* v_scale,
                               int64_t b, int64_t h, int64_t n, int64_t d,
-                              int pv_kind, void* workspace, size_t workspace_bytes,
+                              int qk_kind, int pv_kind, void* workspace, size_t workspace_bytes,
                               void* out, float* lse, int32_t* s_out,
                               hipStream_t stream);
 

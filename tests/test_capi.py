@@ -74,6 +74,8 @@ def test_sizes_and_padding():
         np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
         doc = ((b * (nt + np_ // 32 + 2 * (np_ // 128)) + 1 + 2) * 16 + 255) // 256 * 256
         assert lib.sage_attn_workspace_bytes(b, h, n, d) == doc + pieces * (128 * d + 512) * 4
+        # a masked launch splits no item: the summaries only
+        assert lib.sage_attn_masked_workspace_bytes(b, h, n, d) == doc
 
 
 def _quant_call(lib, **over):
@@ -381,6 +383,9 @@ def test_noalloc_entry_rejects_shapes_beyond_its_scratch():
     lib = _lib.load()
     assert lib.sage_attn_workspace_bytes(1, 32, 4480, 128) > 16 << 20
     assert lib.sage_attn_workspace_bytes(1, 30, 4416, 128) <= 16 << 20
+    # masked launches need the summaries only (the packed 1x30x6912 batch: 7 KB)
+    assert lib.sage_attn_masked_workspace_bytes(1, 30, 6912, 128) == 7168
+    assert lib.sage_attn_masked_workspace_bytes(1, 32, 4480, 128) <= 16 << 20
     args = [16, 32, 48, 64, 80, 96, 1, 32, 4480, 128, 0, 1, 0, None, 0, 0, 0, None, 112, 0, 128, None]
     assert lib.sage_attn_fwd_noalloc(*args) == 3
     assert "beyond the 16777216-byte scratch" in lib.sage_last_error().decode()

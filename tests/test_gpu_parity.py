@@ -133,6 +133,72 @@ def test_attention_kernel_int32_accumulators_headline_split_tail(cuda):
     del s
 
 
+def _sharp_inputs(D, N=1000, B=1, H=2, seed=123):
+    """Scores that rise along the keys: K rows carry a growing multiple of a
+    direction every query shares, so each row's maximum moves by more than 8
+    log2 units several times after the first tile and a few keys carry most
+    of a row's weight."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(D, generator=g)
+    u /= u.norm()
+    q = (2 * math.sqrt(D) * u + torch.randn(B, H, N, D, generator=g)).bfloat16()
+    k = (torch.linspace(0, 14, N).view(1, 1, N, 1) * u + torch.randn(B, H, N, D, generator=g)).bfloat16()
+    v = torch.randn(B, H, N, D, generator=g).bfloat16()
+    return q, k, v
+
+
+# fp32 sums of 128 (or 64) products of e4m3 values: the MFMA's result lies
+# within this fraction of sum |q_i k_i| of the exact sum (recursive summation
+# of n terms stays within n * 2^-24 of it; 2^-16 covers n = 128 with room)
+FP8_QK_REL = 2.0 ** -16
+
+
+@pytest.mark.parametrize("D,sharp", [(128, False), (64, False), (128, True), (64, True)])
+def test_fp8_qk_accumulators_and_kernel_scores(cuda, D, sharp):
+    """fp8 QK: the fp32 S^T sums the kernel's loop consumes (stored from
+    inside it) equal the exact fp64 dot products of the oracle's codes
+    (sage_kernels.py:282) within the fp32 summation bound.
+
+    The oracle's attention (fp8 P.V, reference per-(row, 64-key block) P
+    scaling) run on those same sums, dequantized as the reference does
+    (sage_kernels.py:1451-1453), must then meet the tight bound.  At sharp
+    scores one P code carries most of a row, and a last-ulp difference of an
+    fp32 MFMA sum moves it across an e4m3 rounding boundary (max-abs 0.055
+    against the oracle fed the exact sums): the kernel's own sums remove
+    that difference from the comparison."""
+    SA = _sa()
+    B, H, N = 1, 2, 1000
+    if sharp:
+        q, k, v = _sharp_inputs(D, N, B, H)
+    else:
+        q, k, v = O.make_inputs(B, H, N, D, seed=41 + D)
+    print(f"fp8 QK accumulators D={D} sharp={sharp}", flush=True)
+    qz = SA.quantize_qkv(q.to(cuda), k.to(cuda), v.to(cuda), qk="fp8", pv="fp8")
+    out, lse, s = SA.qk_accumulators(qz, B, H)
+    out2, lse2 = SA.attn_from_quantized(qz, B, H)
+    torch.cuda.synchronize()
+    _assert_bits_equal(out, out2, "out of the accumulator launch")
+    _assert_bits_equal(lse, lse2, "lse of the accumulator launch")
+    oz = O.quantize_all(q, k, v, 1.0 / math.sqrt(D), "fp8", "fp8", "token", True)
+    got = s[:, :N, :N].cpu().double()
+    exact = O.qk_fp8(oz.qc, oz.kc)
+    mag = torch.matmul(oz.qc.double().abs(), oz.kc.double().abs().transpose(1, 2))
+    err = (got - exact).abs()
+    ratio = (err / mag.clamp_min(1e-30)).max().item()
+    print(f"  max |s - exact| / sum|q k| = {ratio:.3g} (bound {FP8_QK_REL:.3g}); "
+          f"{int((err > 0).sum())} of {err.numel()} sums inexact", flush=True)
+    assert ratio <= FP8_QK_REL
+    # the oracle's attention on the kernel's own sums
+    sc = (got.float() * oz.qs[:, :, None]) * oz.ks[:, None, :]
+    ref, ref_lse = O.attend(sc, v.reshape(B * H, N, D), "fp8", None, oz.vc, oz.vs)
+    outf = out.float().cpu().reshape(B * H, N, D)
+    tmax = (outf - ref.float()).abs().max().item()
+    tcos = O.cosine(outf, ref)
+    lerr = (lse.cpu() - ref_lse).abs().max().item()
+    print(f"  vs the oracle on the kernel's sums: max-abs {tmax:.3g} cosine {tcos:.7f} lse {lerr:.3g}", flush=True)
+    assert tmax <= TIGHT_MAXABS and tcos >= TIGHT_COS and lerr <= LSE_TOL
+
+
 def _compare(out, lse, q, k, v, qk, pv, gran, block_mask=None, doc_ids=None, smooth=True, tight=True):
     ref, ref_lse, _ = O.sage_forward(q, k, v, None, qk, pv, gran, smooth, block_mask, doc_ids)
     out = out.float().cpu()
@@ -207,21 +273,19 @@ def test_frame_moves_inside_the_loop(cuda, qk, pv, D):
     and the next (bf16 P.V: a move decided by one tile's softmax is applied
     before the following product is added).
 
-    fp8 QK with fp8 P is left out: at scores this sharp one P code carries
-    most of a row's weight, and a last-ulp difference of an fp8 MFMA sum
-    moves it across an e4m3 rounding boundary (max-abs 0.055 against the
-    emulation, LSE within 1.2e-4); its loop is the int8 case's.  With fp8 QK
+    fp8 QK with fp8 P is left out here: at scores this sharp one P code
+    carries most of a row's weight, and a last-ulp difference of an fp32
+    MFMA sum moves it across an e4m3 rounding boundary (max-abs 0.055
+    against the emulation fed the exact sums, LSE within 1.2e-4).
+    test_fp8_qk_accumulators_and_kernel_scores runs these inputs with fp8 QK
+    and fp8 P against the oracle fed the kernel's own sums, at the tight
+    bound; its loop is the int8 case's.  With fp8 QK
     the tight check against the kernel-scheme emulation is left out too: one
     row's output here follows a few keys' V and reaches magnitude 2-4, where
     one bf16 step (0.0156) is above the tight bound."""
     SA = _sa()
     B, H, N = 1, 2, 1000
-    g = torch.Generator().manual_seed(123)
-    u = torch.randn(D, generator=g)
-    u /= u.norm()
-    q = (2 * math.sqrt(D) * u + torch.randn(B, H, N, D, generator=g)).bfloat16()
-    k = (torch.linspace(0, 14, N).view(1, 1, N, 1) * u + torch.randn(B, H, N, D, generator=g)).bfloat16()
-    v = torch.randn(B, H, N, D, generator=g).bfloat16()
+    q, k, v = _sharp_inputs(D, N, B, H)
     # the inputs do what the test needs: block maxima past the first tile
     # exceed the running reference point by more than 8 (log2 units)
     kf = k.float() - k.float().mean(2, keepdim=True)

@@ -391,3 +391,72 @@ def test_static_p_scheme_close_to_reference_scheme():
     b, lb, _ = O.sage_forward(q, k, v, None, "int8", "fp8", "token", True, p_scheme="static", tau=2.0)
     assert O.cosine(a, b) > 0.999 and (a.float() - b.float()).abs().max() < 2e-2
     assert (la - lb).abs().max() < 1e-4
+
+
+# ---------------------------------------------------------------------------
+# fp8 P.V: one P scale per (row, 64-key block), known answers
+# ---------------------------------------------------------------------------
+
+def _fp8_pv_known_answer_case(offset):
+    """One query row over two 64-key tiles whose live scores are exact
+    integers (log2 units): s = -j for keys j = 0..15 of tile 0 and
+    s = offset - j for keys 64 + j, j = 0..15, of tile 1; the other keys sit
+    at -200 (p = 0 exactly in fp32).  V is the 128 x 128 identity, so output
+    channel c is key c's share: out[c] = p_c / l with p_c = 2^(s_c - max s).
+
+    Per (row, block) P scaling (sage_kernels.py:1137-1141) maps each tile's
+    largest p to 448 and the rest to 448 * 2^-j, which e4m3 holds exactly for
+    j <= 15 (7 * 2^(6 - j), subnormal below 2^-6), in both tiles.  One scale
+    per row across tiles would instead give tile 1 the codes
+    e4m3(448 * 2^(offset - j)): for offset = -12 those fall below e4m3's
+    subnormal grid from j = 4 on (3.5 * 2^-9 rounds to 4 * 2^-9, ...)."""
+    nk, d = 128, 128
+    s = torch.full((1, 1, nk), -200.0)
+    j = torch.arange(16, dtype=torch.float32)
+    s[0, 0, :16] = -j
+    s[0, 0, 64:80] = offset - j
+    v = torch.eye(nk, d).bfloat16().unsqueeze(0)
+    # V codes and scales from the definition (sage_kernels.py:1143-1148):
+    # each channel's block max is 1, so its code is e4m3(448) = 448 and its
+    # scale 1/448; channels with no key in a block have code 0 and scale 0
+    vc = (torch.eye(nk, d) * 448.0).to(torch.float8_e4m3fn).unsqueeze(0)
+    vs = torch.zeros(1, 2, d)
+    vs[0, 0, :64] = torch.tensor(1.0 / 448.0, dtype=torch.float32)
+    vs[0, 1, 64:] = torch.tensor(1.0 / 448.0, dtype=torch.float32)
+    sd = s.double()
+    p = torch.exp2(sd - sd.max())
+    # keys at -200 have p = 0 in fp32, as the reference's exp2 gives them
+    p = torch.where(sd > -100, p, torch.zeros(()))
+    want = (p / p.sum())[0, 0]
+    want_lse = float(sd.max() + torch.log2(p.sum()))
+    return s, v, vc, vs, want, want_lse
+
+
+def _rel_err(out, want):
+    live = want > 0
+    return ((out.double()[live] - want[live]).abs() / want[live]).max().item(), out.double()[~live].abs().max().item()
+
+
+@pytest.mark.parametrize("offset", [-12.0, 12.0])
+def test_attend_fp8_pv_per_block_p_scale_known_answer(offset):
+    """The oracle's fp8 P.V against the closed form: every live key's output
+    share within one bf16 rounding, dead keys exactly 0, LSE within fp32
+    rounding.  offset = +12 moves the row max in tile 1 (alpha = 2^-12 on
+    tile 0's products); offset = -12 leaves it in tile 0."""
+    s, v, vc, vs, want, want_lse = _fp8_pv_known_answer_case(offset)
+    out, lse = O.attend(s, v, "fp8", None, vc, vs)
+    rel, dead = _rel_err(out[0, 0], want)
+    assert rel <= 2.0 ** -8, rel
+    assert dead == 0.0
+    assert abs(float(lse[0, 0]) - want_lse) < 1e-6
+
+
+def test_fp8_pv_known_answer_fails_one_scale_per_row():
+    """The same closed form rejects one P scale per row across tiles (the
+    running-max frame: pc = e4m3(448 * p) with p relative to the row's
+    running max).  The oracle's "static" scheme with tau = 0 is exactly that
+    mistake here: its reference point is set by tile 0 and never moves."""
+    s, v, vc, vs, want, _ = _fp8_pv_known_answer_case(-12.0)
+    out, _ = O.attend(s, v, "fp8", None, vc, vs, p_scheme="static", tau=0.0)
+    rel, _ = _rel_err(out[0, 0], want)
+    assert rel > 0.1, rel

@@ -4,8 +4,11 @@ Both are called through the C ABI on the same quantized operands; the
 allocation-free one keeps its workspace in the library's fixed device scratch.
 Two calls in a row, the second smaller (and with document ids, so the scratch
 then holds other data than the first call left there), must each give the
-outputs and LSE of sage_attn_fwd bit for bit.  (A shape whose workspace
-exceeds the scratch is rejected before any device call: tests/test_capi.py.)
+outputs and LSE of sage_attn_fwd bit for bit.  The packed 1x30x6912 batch
+(1280 + 1216 + 4416 tokens) runs with its tile mask and with exact document
+ids: masked launches need only the summaries, so it fits the scratch although
+its unmasked workspace would not.  (A shape whose workspace exceeds the
+scratch is rejected before any device call: tests/test_capi.py.)
 """
 
 
@@ -29,20 +32,24 @@ def _noalloc(lib, qz, B, H, out, lse, block_mask=None, doc_ids=None, stream=None
         lse.data_ptr(), torch.cuda.current_stream().cuda_stream if stream is None else stream)
 
 
-def _case(cuda, lib, B, H, N, D, seed, pv, doc_segments=None):
+def _case(cuda, lib, B, H, N, D, seed, pv, doc_segments=None, tile_segments=None):
     from futudiffu_amd import block_mask as BM
     from futudiffu_amd import sage_attention as SA
-    assert lib.sage_attn_workspace_bytes(B, H, N, D) <= SCRATCH_BYTES
+    masked = doc_segments is not None or tile_segments is not None
+    need = (lib.sage_attn_masked_workspace_bytes if masked else lib.sage_attn_workspace_bytes)(B, H, N, D)
+    assert need <= SCRATCH_BYTES
     q, k, v = (t.to(cuda) for t in O.make_inputs(B, H, N, D, seed=seed))
-    doc = None
+    doc = bm = None
     if doc_segments is not None:
         doc = BM.build_doc_ids(doc_segments, N, device="cpu", batch=B).to(cuda)
+    if tile_segments is not None:
+        bm = O.build_block_mask(tile_segments, N).to(cuda)
     qz = SA.quantize_qkv(q, k, v, qk="int8", pv=pv)
-    want, want_lse = SA.attn_from_quantized(qz, B, H, doc_ids=doc)
+    want, want_lse = SA.attn_from_quantized(qz, B, H, block_mask=bm, doc_ids=doc)
     # fill values that a missing store would leave visible
     out = torch.full((B, H, N, D), float("nan"), dtype=torch.bfloat16, device=cuda)
     lse = torch.full((B * H, N), float("nan"), dtype=torch.float32, device=cuda)
-    st = _noalloc(lib, qz, B, H, out, lse, doc_ids=doc)
+    st = _noalloc(lib, qz, B, H, out, lse, block_mask=bm, doc_ids=doc)
     assert st == 0, lib.sage_last_error().decode()
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), want.view(torch.int16)), "outputs differ from sage_attn_fwd"
@@ -58,3 +65,13 @@ def test_noalloc_matches_workspace_entry_two_calls(cuda):
     # smaller, with document ids: the summaries now occupy the scratch's start
     print("noalloc call 2: 1x2x1000x128 int8/bf16 with document ids", flush=True)
     _case(cuda, lib, 1, 2, 1000, 128, seed=72, pv="bf16", doc_segments=[400, 350, 250])
+
+
+def test_noalloc_packed_batch_masked(cuda):
+    from futudiffu_amd import _lib
+    lib = _lib.load()
+    segs = [1280, 1216, 4416]
+    print("noalloc packed 1x30x6912x128 int8/fp8 with document ids", flush=True)
+    _case(cuda, lib, 1, 30, 6912, 128, seed=73, pv="fp8", doc_segments=segs)
+    print("noalloc packed 1x30x6912x128 int8/fp8 with the tile mask", flush=True)
+    _case(cuda, lib, 1, 30, 6912, 128, seed=74, pv="fp8", tile_segments=segs)
