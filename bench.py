@@ -66,6 +66,10 @@ def parse():
     ap.add_argument("--stream-calibration", action="store_true",
                     help="instead of the benchmark, time a 2:1 read/write stream at the quantization's "
                          "traffic and at 1 GiB, warm and cold")
+    ap.add_argument("--phase-timing", action="store_true",
+                    help="instead of the benchmark, run the headline op with the measurement build "
+                         "(futudiffu_amd/build.py --phase-timing) and print the per-phase ticks of the "
+                         "attention kernel's pipelined loop")
     ap.add_argument("--all-configs", action="store_true",
                     help="one JSON line per benchmark configuration instead of the headline line")
     ap.add_argument("--cases", default="",
@@ -677,6 +681,69 @@ def all_configs(args):
         print(json.dumps(line), flush=True)
 
 
+PHASE_NAMES = ["loop overhead", "stage loads issued + pending P.V + score conversion", "next QK^T issue",
+               "row max + frame decision", "exp + row sums + P packing", "stage-load wait + barrier"]
+
+
+def phase_timing(args):
+    """Per-phase s_memtime ticks of the attention kernel's pipelined loop
+    (one iteration = one 32-row x 64-key tile of one wave), summed over every
+    live wave of --steps headline calls, from the measurement library.  The
+    scheduling fences at the phase boundaries keep each phase's instructions
+    inside it, so the instrumented kernel runs slower than the product one;
+    the split shows where a wave's time goes."""
+    import ctypes
+    root = os.path.dirname(os.path.abspath(__file__))
+    path = os.path.join(root, "futudiffu_amd", "libsage_mi355x_phase.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: python futudiffu_amd/build.py --phase-timing")
+    os.environ["SAGE_MI355X_LIB"] = path
+    sys.path.insert(0, root)
+    from futudiffu_amd import _lib
+    from futudiffu_amd import sage_attention as SA
+    lib = _lib.load()
+    lib.sage_phase_read.restype = ctypes.c_int
+    lib.sage_phase_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    B, H, N, D = args.B, args.H, args.N, args.D
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q = torch.randn(B, H, N, D, generator=g).bfloat16().to(dev)
+    k = (torch.randn(B, H, N, D, generator=g) + 2.0 * torch.randn(B, H, 1, D, generator=g)).bfloat16().to(dev)
+    v = torch.randn(B, H, N, D, generator=g).bfloat16().to(dev)
+    qz = SA.quantize_qkv(q, k, v, 1.0 / math.sqrt(D), qk=args.qk, pv=args.pv, granularity=args.granularity)
+    prewarm(lambda: SA.attn_from_quantized(qz, B, H), args.prewarm_seconds)
+    torch.cuda.synchronize()
+    if lib.sage_phase_read(None, 0, 1) != 0:
+        raise RuntimeError("sage_phase_read failed")
+    evs = [(TimingEvent(), TimingEvent()) for _ in range(args.steps)]
+    for e in evs:
+        e[0].record()
+        SA.attn_from_quantized(qz, B, H)
+        e[1].record()
+    torch.cuda.synchronize()
+    slots = 32768
+    buf = (ctypes.c_ulonglong * (slots * 8))()
+    if lib.sage_phase_read(buf, slots * 8, 1) != 0:
+        raise RuntimeError("sage_phase_read failed")
+    rows = [buf[i * 8:(i + 1) * 8] for i in range(slots)]
+    rows = [r for r in rows if r[6] > 0]
+    iters = sum(r[6] for r in rows)
+    tot = [sum(r[k] for r in rows) for k in range(6)]
+    loop_ticks = sum(r[7] for r in rows)
+    per = [t / iters for t in tot]
+    ms = sorted(e[0].elapsed_time(e[1]) for e in evs)[len(evs) // 2]
+    print(json.dumps({
+        "phase_timing": f"attn_fwd_kernel {args.qk}-QK {args.pv}-PV B={B} H={H} N={N} D={D}, {args.steps} calls",
+        "instrumented_kernel_ms_median": round(ms, 5),
+        "waves_timed": len(rows), "iterations": iters,
+        "ticks_per_iteration": round(sum(per), 1),
+        "phases": [{"phase": PHASE_NAMES[k], "ticks_per_iteration": round(per[k], 1),
+                    "share": round(per[k] / sum(per), 4)} for k in range(6)],
+        "loop_ticks_outside_timed_iterations_share": round(1 - sum(tot) / loop_ticks, 4),
+        "unit": "s_memtime ticks per wave per 32x64 tile",
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -691,6 +758,9 @@ def main():
         return
     if args.stream_calibration:
         stream_calibration(args)
+        return
+    if args.phase_timing:
+        phase_timing(args)
         return
     if args.all_configs:
         all_configs(args)

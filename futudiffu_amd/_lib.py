@@ -11,7 +11,10 @@ import ctypes
 import os
 import threading
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsage_mi355x.so")
+# SAGE_MI355X_LIB selects another build of the same library (the measurement
+# build, futudiffu_amd/build.py --phase-timing)
+LIB_PATH = os.environ.get("SAGE_MI355X_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                             "libsage_mi355x.so")
 
 # Every symbol include/sage_mi355x.h declares, with its ctypes signature.
 _c = ctypes

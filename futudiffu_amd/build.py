@@ -19,6 +19,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libsage_mi355x.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
+# the measurement build: the same library with per-phase s_memtime timing of
+# the attention kernel's pipelined loop (sage_phase_read), for bench.py
+# --phase-timing; never loaded by the product path
+PHASE_LIB_PATH = os.path.join(HERE, "libsage_mi355x_phase.so")
 SOURCES = ["sage_quant.hip", "sage_attn.hip", "sage_mask.hip", "sage_bwd.hip", "sage_capi.hip"]
 ARCH = "gfx950"
 
@@ -48,15 +52,18 @@ def _link(cc: str, objs: list[str], tmp: str, path: str) -> None:
     os.replace(path + ".tmp", path)
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source and link LIB_PATH atomically; returns LIB_PATH."""
+def build(verbose: bool = False, phase_timing: bool = False) -> str:
+    """Compile every source and link LIB_PATH atomically; returns LIB_PATH.
+    With phase_timing, builds PHASE_LIB_PATH (-DSAGE_PHASE_TIMING) instead."""
     cc = hipcc()
+    extra = ["-DSAGE_PHASE_TIMING"] if phase_timing else []
+    out_path = PHASE_LIB_PATH if phase_timing else LIB_PATH
     with tempfile.TemporaryDirectory(prefix="sage_build_") as tmp:
         srcs = SOURCES
         objs = [os.path.join(tmp, src + ".o") for src in srcs]
 
         def compile_one(i: int) -> None:
-            cmd = [cc, *flags(), "-c", os.path.join(CSRC, srcs[i]), "-o", objs[i]]
+            cmd = [cc, *flags(), *extra, "-c", os.path.join(CSRC, srcs[i]), "-o", objs[i]]
             if verbose:
                 print(" ".join(cmd), flush=True)
             res = subprocess.run(cmd, capture_output=True, text=True)
@@ -67,9 +74,9 @@ def build(verbose: bool = False) -> str:
         with concurrent.futures.ThreadPoolExecutor(max_workers=min(4, len(srcs))) as pool:
             for f in [pool.submit(compile_one, i) for i in range(len(srcs))]:
                 f.result()
-        _link(cc, objs, tmp, LIB_PATH)
-    return LIB_PATH
+        _link(cc, objs, tmp, out_path)
+    return out_path
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, phase_timing="--phase-timing" in sys.argv))

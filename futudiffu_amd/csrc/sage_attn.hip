@@ -47,6 +47,29 @@
 
 namespace sage {
 
+// Per-phase timing of the pipelined loop, built only into the measurement
+// library (SAGE_PHASE_TIMING; futudiffu_amd/build.py --phase-timing): every
+// live wave accumulates s_memtime ticks per phase of each loop iteration
+// (scheduling fences keep each phase's instructions inside it) and stores
+// them, with its iteration count, to one slot per (workgroup, wave).
+#ifdef SAGE_PHASE_TIMING
+constexpr int kPhaseSlots = 32768;
+constexpr int kPhases = 6;  // slot words 0..5 phases, 6 iterations, 7 ticks in the loop
+__device__ unsigned long long sage_phase_buf[kPhaseSlots][8];
+#define SAGE_PHASE(k)                                      \
+  do {                                                     \
+    __builtin_amdgcn_sched_barrier(0);                     \
+    const uint64_t now_ = __builtin_amdgcn_s_memtime();    \
+    ph_acc[k] += now_ - ph_last;                           \
+    ph_last = now_;                                        \
+    __builtin_amdgcn_sched_barrier(0);                     \
+  } while (0)
+#else
+#define SAGE_PHASE(k) \
+  do {                \
+  } while (0)
+#endif
+
 constexpr float kLog2Fp8Max = 8.807354922057604f;  // log2(448)
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 
@@ -170,6 +193,27 @@ __device__ __forceinline__ void item_of(int id, int total, int bh_count, int nq,
   }
 }
 
+// The int8 QK^T accumulates on top of the bit pattern of c0 = 1/(2 pi) (the
+// C operand of each chain's first MFMA; the compiler keeps the splat in
+// registers rather than encoding the inline constant).  |acc| <= 128 *
+// 127^2 < 2^21 keeps c0_bits + acc inside c0's binade [1/8, 1/4), whose ulp
+// is 2^-26, so the accumulator read as fp32 is exactly x = c0 + acc * 2^-26,
+// and x - c0 = acc * 2^-26 exactly (Sterbenz).  One subtraction of the
+// inline constant replaces the int -> float conversion (v_cvt_f32_i32 issues
+// at about half the rate of a subtraction); the 2^26 goes into the row's
+// multiplier, so scores, maxima and exp arguments are the same floats as
+// float(acc) * kd * w gives (powers of two scale exactly for row
+// multipliers below 2^101).
+constexpr int32_t kC0Bits = 0x3E22F983;
+constexpr float kC0 = 0.15915494309189535f;
+static_assert(__builtin_bit_cast(int32_t, kC0) == kC0Bits, "c0 must be the inline constant 1/(2 pi)");
+constexpr float kC0Scale = 67108864.0f;  // 2^26, the accumulator's ulp inverted
+// the C operand of a chain's first int8 MFMA
+__device__ __forceinline__ i32x16 c0_acc() {
+  return i32x16{kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits,
+                kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits};
+}
+
 template <int QK>
 struct SAccT {
   using type = f32x16;
@@ -187,10 +231,10 @@ __device__ __forceinline__ void qk_half(const uint8_t* sb, const i32x4* qf, int 
   constexpr int NC = D / 32;
   const i32x4* kl = reinterpret_cast<const i32x4*>(sb);
   if constexpr (QK == kQK_INT8) {
-    acc = i32x16{0};
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(b * NC + c) * 64 + lane], qf[c], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(b * NC + c) * 64 + lane], qf[c], c == 0 ? c0_acc() : acc,
+                                                  0, 0, 0);
   } else {
     acc = f32x16{0};
 #pragma unroll
@@ -219,13 +263,11 @@ __device__ __forceinline__ void qk_both(const uint8_t* sb, const i32x4* qf, int 
     };
     read(0);
     read(1);
-    a0 = i32x16{0};
-    a1 = i32x16{0};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       __builtin_amdgcn_sched_barrier(0);
-      a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0][c], qf[c], a0, 0, 0, 0);
-      a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1][c], qf[c], a1, 0, 0, 0);
+      a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0][c], qf[c], c == 0 ? c0_acc() : a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1][c], qf[c], c == 0 ? c0_acc() : a1, 0, 0, 0);
       if (c + 2 < NC) read(c + 2);
     }
   } else {
@@ -274,7 +316,12 @@ __device__ __forceinline__ void half_scores(const uint8_t* sb, const typename SA
     else
       kd4 = f32x4{kd_blk, kd_blk, kd_blk, kd_blk};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) u[4 * j + i] = (float)s[4 * j + i] * kd4[i];
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (QK == kQK_INT8)
+        u[4 * j + i] = (__int_as_float(s[4 * j + i]) - kC0) * kd4[i];  // acc * kd * 2^-26
+      else
+        u[4 * j + i] = s[4 * j + i] * kd4[i];
+    }
   }
   if (kvalid < 64) {
 #pragma unroll
@@ -419,10 +466,10 @@ __device__ __forceinline__ void softmax_fp8_exp_qk(const float (&u)[2][16], floa
   l_acc = fmaf(rsc, (es[0] + es[1]) + (es[2] + es[3]), l_acc);
 }
 
-template <int D>
-__device__ __forceinline__ void softmax_fp8(float (&u)[2][16], float wt, float& m_ref, float& l_acc, f32x16* o,
-                                            float* xrow, int h, int r, i32x8& pa, float& rsc) {
-  const float bm = row_max_move<D>(u, wt, m_ref, l_acc, o, xrow, h, r);
+// The exp / pack part of the fp8 softmax after the frame decision for block
+// max bm: P codes into pa, the row factor into rsc, the row sum into l.
+__device__ __forceinline__ void softmax_fp8_exp(const float (&u)[2][16], float wt, float bm, float m_ref,
+                                                float& l_acc, i32x8& pa, float& rsc) {
   const bool row_live = bm > -INFINITY;
   rsc = row_live ? __builtin_amdgcn_exp2f(bm - m_ref) * (1.0f / kFp8Max) : 0.0f;
   const float bias = row_live ? (kLog2Fp8Max - bm) : 0.0f;  // masked u are -inf: e = 0
@@ -440,6 +487,13 @@ __device__ __forceinline__ void softmax_fp8(float (&u)[2][16], float wt, float& 
       pa[4 * b + j] = (int)pack_fp8x4(e4[0], e4[1], e4[2], e4[3]);
     }
   l_acc = fmaf(rsc, (es[0] + es[1]) + (es[2] + es[3]), l_acc);
+}
+
+template <int D>
+__device__ __forceinline__ void softmax_fp8(float (&u)[2][16], float wt, float& m_ref, float& l_acc, f32x16* o,
+                                            float* xrow, int h, int r, i32x8& pa, float& rsc) {
+  const float bm = row_max_move<D>(u, wt, m_ref, l_acc, o, xrow, h, r);
+  softmax_fp8_exp(u, wt, bm, m_ref, l_acc, pa, rsc);
 }
 
 // fp8 P.V of one tile for the chunk pair (c2, c2 + 1): the block products
@@ -626,7 +680,9 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     qd = p.qs[(int64_t)bh * p.np + q0 + r];
   else
     qd = p.qs[(int64_t)bh * (p.np / 64) + (q0 >> 6)];
-  const float w = fmaxf(qd, 1e-30f);  // log2-domain multiplier of the (K-scaled) accumulators
+  // log2-domain multiplier of the (K-scaled) accumulators; int8 QK scores
+  // carry 2^-26 (the c0 start), which the multiplier takes back exactly
+  const float w = fmaxf(qd, 1e-30f) * (QK == kQK_INT8 ? kC0Scale : 1.0f);
 
   int dq = 0;
   int4 qsum = make_int4(0, 0, 0, 0), qsum128 = make_int4(0, 0, 0, 0);
@@ -723,7 +779,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     if constexpr (DUMP) {
       int32_t* row = p.s_dump + ((int64_t)bh * p.np + q0 + r) * p.np + (int64_t)tt * 64 + 4 * h;
       auto word = [](auto x) -> int32_t {
-        if constexpr (QK == kQK_INT8) return x;
+        if constexpr (QK == kQK_INT8) return x - kC0Bits;  // the sum itself
         else return __float_as_int(x);
       };
 #pragma unroll
@@ -873,6 +929,12 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
       return !listed;
     }
     const bool any = t < t_end;
+#ifdef SAGE_PHASE_TIMING
+    uint64_t ph_acc[kPhases] = {0, 0, 0, 0, 0, 0};
+    uint64_t ph_last = __builtin_amdgcn_s_memtime();
+    const uint64_t ph_start = ph_last;
+    int ph_n = 0;
+#endif
     // the pending product: fp8 P codes and their row factor, or bf16 P and
     // the frame move that precedes its accumulation
     i32x8 pa_p = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -928,6 +990,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     }
     // one iteration for a whole tile t with a successor
     auto iteration = [&]() __attribute__((always_inline)) {
+      SAGE_PHASE(0);  // loop overhead since the last iteration's end
       issue_loads();
       const uint8_t* sb = sp(stage);
       const uint8_t* sbp = sp(stage_p);
@@ -971,17 +1034,30 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
         const float bm = row_max_move<D>(u, w, m_ref, l_acc, o, xrow, h, r);
         softmax_fp8_exp_qk<D>(u, w, bm, m_ref, l_acc, pa_p, rsc_p, sp(next_stage(stage, 1)), qf, lane, s0, s1);
       } else {
+        SAGE_PHASE(1);  // the pending product and this tile's score conversion
         qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
         if constexpr (PV == kPV_BF16) {
           if constexpr (QK != kQK_INT8) pv_bf16_pair<D>(sbp, pb_p, lane, 0, o);
           if constexpr (NP == 2) pv_bf16_pair<D>(sbp, pb_p, lane, 2, o);
         }
+        SAGE_PHASE(2);  // the next tile's QK^T issue
         prefetch_pending();
-        softmax_p();
+        if constexpr (PV == kPV_FP8) {
+          const float bm = row_max_move<D>(u, w, m_ref, l_acc, o, xrow, h, r);
+          SAGE_PHASE(3);  // row max and frame decision
+          softmax_fp8_exp(u, w, bm, m_ref, l_acc, pa_p, rsc_p);
+        } else {
+          softmax_p();
+        }
+        SAGE_PHASE(4);  // exp, row sums, P packing
       }
       stage_p = stage;
       publish();
+      SAGE_PHASE(5);  // stage loads complete, workgroup barrier
       advance();
+#ifdef SAGE_PHASE_TIMING
+      ++ph_n;
+#endif
     };
     // the pending product, one chunk pair's products in flight at a time
     auto flush = [&]() __attribute__((always_inline)) {
@@ -1005,6 +1081,18 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     } else if (any) {  // the single tile was also the first: its product is pending
       flush();
     }
+#ifdef SAGE_PHASE_TIMING
+    {
+      const uint64_t ph_end = __builtin_amdgcn_s_memtime();
+      const int slot = (int)blockIdx.x * 4 + wave;
+      if (lane == 0 && slot < kPhaseSlots) {
+#pragma unroll
+        for (int k = 0; k < kPhases; ++k) sage_phase_buf[slot][k] += ph_acc[k];
+        sage_phase_buf[slot][6] += (unsigned long long)ph_n;
+        sage_phase_buf[slot][7] += ph_end - ph_start;
+      }
+    }
+#endif
     __syncthreads();  // the ring is reused after
     return !listed;
   }
@@ -1385,3 +1473,22 @@ size_t attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d, bool mas
 }
 
 }  // namespace sage
+
+#ifdef SAGE_PHASE_TIMING
+// Measurement library only: copies min(count, slots * 8) words of the phase
+// buffer to host memory, then clears the buffer when clear != 0.
+extern "C" int sage_phase_read(unsigned long long* host, size_t count, int clear) {
+  const size_t words = (size_t)sage::kPhaseSlots * 8;
+  if (count > words) count = words;
+  if (host && count &&
+      hipMemcpyFromSymbol(host, HIP_SYMBOL(sage::sage_phase_buf), count * 8, 0, hipMemcpyDeviceToHost) != hipSuccess)
+    return -1;
+  if (clear) {
+    void* dev = nullptr;
+    if (hipGetSymbolAddress(&dev, HIP_SYMBOL(sage::sage_phase_buf)) != hipSuccess) return -1;
+    if (hipMemset(dev, 0, words * 8) != hipSuccess) return -1;
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+  }
+  return 0;
+}
+#endif
