@@ -151,6 +151,13 @@ __device__ __forceinline__ void row_amax(const float (&x)[PASSES][8], float (&am
 
 // ---- q/k producer (fused_qkv_postprocess, fused_kernels.py:271-390) ---------
 
+// Heads per slab unit: a workgroup that takes one pass of tokens for this many
+// heads of a batch (the last group of a batch may have fewer) loads the
+// tokens' rotation rows once for all of them.  The rotations are 16 bytes per
+// channel pair and token, four times the bf16 data of a head; read per head
+// they made up most of the L2 traffic of the producer-fused quantization.
+constexpr int kSlabHeads = 8;
+
 // Sum over the LPR consecutive lanes (8 or 16) that hold one token's channels:
 // a pairwise tree over the lanes in order, with DPP moves of the two halves of
 // the fp64 value (quad xor 1, quad xor 2, half-row mirror, row mirror, as in
@@ -180,25 +187,69 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Reciprocal RMS of the G tokens (G = 2 or 4) of which a lane holds channels
+// [8*c8, +8) (w[g]: token g), rrms = 1 / sqrt(mean(x^2) + eps) over each
+// token's D channels (fused_kernels.py:316-320), returned in every lane of a
+// quad: lane p of the quad (p < G) holds token p's, so quad_lane_c<g> hands
+// every lane token g's.  The sum of squares is formed in fp64 in a fixed
+// order: each lane's 8 channels left to right (the squares are exact), then a
+// pairwise tree over the token's LPR lanes: lanes l and l^1, then l and l^2
+// (quad sums), then quads q and q^1, then (LPR 16) half-rows; rounded once to
+// fp32.  The tree is reduce-scattered over the G tokens: at its first level a
+// lane keeps tokens {b0, b0 + 2} (b0 = lane bit 0) and hands the other two to
+// its partner, at the second it keeps token b0 + 2*b1, so the two levels cost
+// G/2 + 1 adds instead of 2G; the quad levels run on the one token left
+// (rotating quad r onto r+1 leaves the pair sums in quads 1 and 3 of each
+// 16-lane row).  Then one correctly rounded sqrt and division per lane
+// instead of one per token, and the results of quads 1 and 3 are copied to
+// quads 0 and 2.  fp64 addition is commutative, so every token's sum is the
+// same tree's, bit for bit, whichever lane forms it.
+template <int D, int G>
+__device__ __forceinline__ float tokens_rrms(const uint4 (&w)[G], float eps, int tid) {
+  static_assert(G == 2 || G == 4, "tokens per lane");
+  constexpr int LPR = D / 8;
+  double ss[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float x[8];
+    unpack8(w[g], x);
+    ss[g] = 0.0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss[g] = __builtin_fma((double)x[e], (double)x[e], ss[g]);
+  }
+  const bool b0 = tid & 1, b1 = tid & 2;
+  double s;
+  if constexpr (G == 4) {
+    // lanes l, l^1: keep tokens b0 and b0 + 2, hand over b0^1 and (b0^1) + 2
+    const double a0 = (b0 ? ss[1] : ss[0]) + dpp_f64<0xB1>(b0 ? ss[0] : ss[1]);
+    const double a2 = (b0 ? ss[3] : ss[2]) + dpp_f64<0xB1>(b0 ? ss[2] : ss[3]);
+    // lanes l, l^2: keep token b0 + 2*b1
+    s = (b1 ? a2 : a0) + dpp_f64<0x4E>(b1 ? a0 : a2);
+  } else {
+    s = (b0 ? ss[1] : ss[0]) + dpp_f64<0xB1>(b0 ? ss[0] : ss[1]);  // keep token b0
+    s += dpp_f64<0x4E>(s);
+  }
+  // quads q and q^1 of the token: quad r reads quad r - 1 (row_ror:4), valid
+  // in quads 1 and 3; LPR 16: half-rows (row_ror:8), valid in quads 1 and 3
+  s += dpp_f64<0x124>(s);
+  if constexpr (LPR == 16) s += dpp_f64<0x128>(s);
+  const float ms = (float)(s / (double)D);
+  float r = 1.0f / sqrtf(ms + eps);  // correctly rounded sqrt and division
+  // quads 0 and 2 (banks 0 and 2) take the next quad's (row_shl:4)
+  r = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(r), __float_as_int(r), 0x104, 0xf, 0x5, false));
+  return r;
+}
+
 // RMSNorm + rotary embedding of the 8 channels [8*c8, +8) of one token held
-// by a lane (bf16 in, bf16 out).  rrms = 1 / sqrt(mean(x^2) + eps) over the
-// token's D channels (fused_kernels.py:316-320; the sum of squares in fp64, in
-// a fixed order: each lane's 8 channels left to right, then a pairwise tree
-// over the token's lanes; rounded once to fp32), n = x * rrms * w (:357-360), and per channel
-// pair (2p, 2p+1) with fr[p] = (cos, -sin, sin) (:334-336):
-// even' = cos*n_even + (-sin)*n_odd, odd' = sin*n_even + cos*n_odd (:363-366),
-// every product and sum a separately rounded fp32 operation.
-template <int D>
-__device__ __forceinline__ uint4 rms_rope8(uint4 w, const float (&nw)[8], const f32x4 (&fr)[4], float eps) {
+// by a lane (bf16 in, bf16 out), with the token's rrms (tokens_rrms):
+// n = x * rrms * w (fused_kernels.py:357-360), and per channel pair (2p, 2p+1)
+// with fr[p] = (cos, -sin, sin) (:334-336): even' = cos*n_even + (-sin)*n_odd,
+// odd' = sin*n_even + cos*n_odd (:363-366), every product and sum a separately
+// rounded fp32 operation.
+__device__ __forceinline__ uint4 rope8(uint4 w, float rrms, const float (&nw)[8], const f32x4 (&fr)[4]) {
 #pragma clang fp contract(off)  // no fused multiply-add: every product and sum rounds on its own
   float x[8];
   unpack8(w, x);
-  double ss = 0.0;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ss = __builtin_fma((double)x[e], (double)x[e], ss);  // the square is exact
-  ss = token_sum<D / 8>(ss);
-  const float ms = (float)(ss / (double)D);
-  const float rrms = 1.0f / sqrtf(ms + eps);  // correctly rounded sqrt and division
   float nn[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) nn[e] = (x[e] * rrms) * nw[e];
@@ -283,41 +334,52 @@ struct HeadRows {
 
 // Standalone producer: bf16 q, k, v [BH, N, D] from the projection output
 // (the outputs of fused_qkv_postprocess, fused_kernels.py:372-385).  One
-// workgroup per (64-token block, bh); lane (rr, c8) holds channels
-// [8*c8, +8) of tokens rr + RPP*ps.
+// workgroup per (pass of RPP tokens, group of kSlabHeads heads of a batch),
+// groups fastest; lane (rr, c8) holds channels [8*c8, +8) of token s0 + rr,
+// loads the token's rotations once and applies them to every head of the
+// group, four heads at a time (one reduce-scattered RMS for the four).
 template <int D>
 __global__ void __launch_bounds__(256) qkv_postprocess_kernel(ProdArgs prod, int64_t n, uint16_t* __restrict__ q_out,
                                                               uint16_t* __restrict__ k_out,
                                                               uint16_t* __restrict__ v_out) {
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
-  constexpr int PASSES = 64 / RPP;
-  int64_t unit;
-  int bh;
-  block_coords<true>(prod, unit, bh);
   const int tid = threadIdx.x;
   const int c8 = tid % LPR, rr = tid / LPR;
-  const int64_t tok0 = unit * 64;
-  const HeadRows<D, true> src(nullptr, nullptr, nullptr, prod, bh, n);
-  float qn[8], kn[8];
-  load_w8(prod.qw, c8, qn);
-  load_w8(prod.kw, c8, kn);
+  const int64_t ngb = (prod.h + kSlabHeads - 1) / kSlabHeads, nsl = (n + RPP - 1) / RPP;
+  const int64_t unit = blockIdx.x;
+  const int64_t bs = unit / ngb;  // b * nsl + slab
+  const int b = (int)(bs / nsl);
+  const int64_t s0 = (bs - (int64_t)b * nsl) * RPP;
+  const int h0 = (int)(unit - bs * ngb) * kSlabHeads, h1 = min(h0 + kSlabHeads, prod.h);
+  const int64_t t = s0 + rr;
+  const bool valid = t < n;
+  const int64_t tc = valid ? t : n - 1;  // clamped: the lanes of a token reduce together
+  f32x4 fr[4];
+  load_freqs<D>(prod.freqs, (int64_t)b * n + tc, c8, fr);
+  const int64_t hd = (int64_t)prod.h * D;
+  const uint16_t* row = prod.qkv + ((int64_t)b * n + tc) * 3 * hd + c8 * 8;
 #pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) {
-    const int64_t t = tok0 + rr + ps * RPP;
-    const int64_t tok = min(t, n - 1);  // clamped: the lanes of a token reduce together
-    const uint4 qw = *reinterpret_cast<const uint4*>(src.q + tok * src.stride + c8 * 8);
-    const uint4 kw = *reinterpret_cast<const uint4*>(src.k + tok * src.stride + c8 * 8);
-    const uint4 vw = *reinterpret_cast<const uint4*>(src.v + tok * src.stride + c8 * 8);
-    f32x4 fr[4];
-    load_freqs<D>(prod.freqs, src.row0 + tok, c8, fr);
-    const uint4 qo = rms_rope8<D>(qw, qn, fr, prod.eps);
-    const uint4 ko = rms_rope8<D>(kw, kn, fr, prod.eps);
-    if (t < n) {
-      const int64_t o = ((int64_t)bh * n + t) * D + c8 * 8;
-      *reinterpret_cast<uint4*>(q_out + o) = qo;
-      *reinterpret_cast<uint4*>(k_out + o) = ko;
-      *reinterpret_cast<uint4*>(v_out + o) = vw;
+  for (int it = 0; it < kSlabHeads / 4; ++it) {
+    const int hb = h0 + 4 * it;
+    if (hb >= h1) break;  // uniform
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      uint16_t* out = m == 0 ? q_out : m == 1 ? k_out : v_out;
+      uint4 w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint4*>(row + m * hd + (int64_t)min(hb + j, h1 - 1) * D);
+      if (m < 2) {
+        const float r = tokens_rrms<D, 4>(w, prod.eps, tid);
+        float nw[8];
+        load_w8(m == 0 ? prod.qw : prod.kw, c8, nw);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = rope8(w[j], quad_lane(r, j), nw, fr);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (valid && hb + j < h1)
+          *reinterpret_cast<uint4*>(out + (((int64_t)b * prod.h + hb + j) * n + t) * D + c8 * 8) = w[j];
     }
   }
 }
@@ -460,13 +522,22 @@ __device__ __forceinline__ void rows_load(const uint16_t* src, int64_t stride, i
   for (int ps = 0; ps < PASSES; ++ps) w[ps] = load16(rs, (uint32_t)(((rr + ps * RPP) * stride + c8 * 8) * 2));
 }
 
+// The producer's inputs for the rows of one head: the norm weights and the
+// rotation rows from `row0` (the flattened (batch, token) index of token 0).
+struct ProdRows {
+  const ProdArgs* prod;
+  const float* nw;
+  int64_t row0;
+};
+
 // Q, or K without smoothing (mu == nullptr), or K smoothed by the head's bf16
 // mean mu[D] (in LDS): codes in row-fragment order and scales of one 64-token
 // block from the loads of rows_load.  PROD: rows of the projection output
-// through RMSNorm + rotary (weights nw).  TAIL: the block reaches past N.
+// through RMSNorm + rotary (pr: the block's weights and rotations).  TAIL: the
+// block reaches past N.
 template <int D, int QK, int GRAN, bool PROD, bool TAIL>
-__device__ __forceinline__ void rows_quant(uint4 (&w)[64 / (256 / (D / 8))], int64_t row0, const float* nw,
-                                           const ProdArgs& prod, int64_t tok0, int64_t n, float fold,
+__device__ __forceinline__ void rows_quant(uint4 (&w)[64 / (256 / (D / 8))], const ProdRows& pr,
+                                           int64_t tok0, int64_t n, float fold,
                                            const float* mu, uint8_t* __restrict__ codes, float* __restrict__ scale,
                                            unsigned* blk_amax, int tid) {
   constexpr int LPR = D / 8;
@@ -474,13 +545,14 @@ __device__ __forceinline__ void rows_quant(uint4 (&w)[64 / (256 / (D / 8))], int
   constexpr int PASSES = 64 / RPP;
   const int c8 = tid % LPR, rr = tid / LPR;
   if constexpr (PROD) {
+    const float r = tokens_rrms<D, PASSES>(w, pr.prod->eps, tid);
     float wn[8];
-    load_w8(nw, c8, wn);
+    load_w8(pr.nw, c8, wn);
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
       f32x4 fr[4];
-      load_freqs<D>(prod.freqs, row0 + min(tok0 + rr + ps * RPP, n - 1), c8, fr);
-      w[ps] = rms_rope8<D>(w[ps], wn, fr, prod.eps);
+      load_freqs<D>(pr.prod->freqs, pr.row0 + min(tok0 + rr + ps * RPP, n - 1), c8, fr);
+      w[ps] = rope8(w[ps], quad_lane(r, ps), wn, fr);
       if (tok0 + rr + ps * RPP >= n) w[ps] = make_uint4(0, 0, 0, 0);  // +0 codes past N
     }
   }
@@ -524,7 +596,8 @@ __device__ __forceinline__ void rows_block(const uint16_t* src, int64_t stride, 
                                            int tid) {
   uint4 w[64 / (256 / (D / 8))];
   rows_load<D>(src, stride, tok0, n, tid, w);
-  rows_quant<D, QK, GRAN, PROD, false>(w, row0, nw, prod, tok0, n, fold, nullptr, codes, scale, blk_amax, tid);
+  rows_quant<D, QK, GRAN, PROD, false>(w, ProdRows{&prod, nw, row0}, tok0, n, fold, nullptr, codes, scale, blk_amax,
+                                       tid);
 }
 
 // V of one 64-token block: per-channel fp8 scales and codes, or bf16, in the
@@ -669,11 +742,12 @@ __device__ __forceinline__ double chunk_colsum(const uint16_t* src, int64_t stri
 #pragma unroll
       for (int i = 0; i < GROUP; ++i) w[i] = load16(rs, (uint32_t)(((rr + (g0 + i) * RPP) * stride + c8 * 8) * 2));
       if constexpr (PROD) {
+        const float r = tokens_rrms<D, GROUP>(w, prod.eps, tid);
 #pragma unroll
         for (int i = 0; i < GROUP; ++i) {
           f32x4 fr[4];
           load_freqs<D>(prod.freqs, row0 + min(t0 + rr + (g0 + i) * RPP, n - 1), c8, fr);
-          w[i] = rms_rope8<D>(w[i], kn, fr, prod.eps);  // zero rows stay zero
+          w[i] = rope8(w[i], quad_lane(r, i), kn, fr);  // zero rows stay zero
         }
       }
 #pragma unroll
@@ -829,16 +903,13 @@ __global__ void __launch_bounds__(256) quantize_k_kernel(const uint16_t* __restr
   head_mean<D>(mean_sum<D>(mt, nch, tid), n, msum, mu, y == 0 ? kmean + (int64_t)bh * D : nullptr, tid);
   const int64_t co = (int64_t)bh * np * D;
   const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+  const ProdRows pr{&prod, prod.kw, src.row0};
   if (tok0 + 128 <= n) {
-    rows_quant<D, QK, GRAN, PROD, false>(w0, src.row0, prod.kw, prod, tok0, n, 1.0f, mu, kc + co, ks + sco,
-                                         &blk_amax[0], tid);
-    rows_quant<D, QK, GRAN, PROD, false>(w1, src.row0, prod.kw, prod, tok0 + 64, n, 1.0f, mu, kc + co, ks + sco,
-                                         &blk_amax[1], tid);
+    rows_quant<D, QK, GRAN, PROD, false>(w0, pr, tok0, n, 1.0f, mu, kc + co, ks + sco, &blk_amax[0], tid);
+    rows_quant<D, QK, GRAN, PROD, false>(w1, pr, tok0 + 64, n, 1.0f, mu, kc + co, ks + sco, &blk_amax[1], tid);
   } else {
-    rows_quant<D, QK, GRAN, PROD, true>(w0, src.row0, prod.kw, prod, tok0, n, 1.0f, mu, kc + co, ks + sco,
-                                        &blk_amax[0], tid);
-    rows_quant<D, QK, GRAN, PROD, true>(w1, src.row0, prod.kw, prod, tok0 + 64, n, 1.0f, mu, kc + co, ks + sco,
-                                        &blk_amax[1], tid);
+    rows_quant<D, QK, GRAN, PROD, true>(w0, pr, tok0, n, 1.0f, mu, kc + co, ks + sco, &blk_amax[0], tid);
+    rows_quant<D, QK, GRAN, PROD, true>(w1, pr, tok0 + 64, n, 1.0f, mu, kc + co, ks + sco, &blk_amax[1], tid);
   }
 }
 
@@ -885,6 +956,109 @@ __device__ __forceinline__ double head_sum_part(bool ready, const HeadRows<D, PR
   return s;
 }
 
+// Waves per SIMD the producer form of quantize_one_kernel is compiled for: its
+// column-sum, slab and fallback paths would take ~117 VGPRs (4 waves) left to
+// themselves; at 5 (at most 102) the compiler reorders instead of spilling,
+// and the kernel runs in 51.5 instead of 58 us at 1x4416x30x128 (6 waves:
+// spills, slower).
+constexpr int kProdWaves = 5;
+
+// Slab units of the producer form with per-token scales: a Q or K unit takes
+// the RPP tokens of one pass (lane (rr, c8): token s0 + rr, channels
+// [8*c8, +8)) for heads [h0, h1) of batch b.  The lane loads its token's
+// rotations once (12 floats) and applies them to every head; the heads go four
+// at a time, the four taking the places of the four tokens of rows_quant: one
+// reduce-scattered RMS (tokens_rrms) and one quantization division per quad
+// serve the four.  K rows are shifted by their head's mean (mu: row h - h0 of
+// D floats); codes, scales and zeros past N are those of rows_quant.
+template <int D, int QK, bool K>
+__device__ __forceinline__ void slab_heads(const ProdArgs& prod, int b, int h0, int h1, int64_t s0, int64_t n,
+                                           int64_t np, float fold, const float* mu, uint8_t* __restrict__ codes,
+                                           float* __restrict__ scale, int tid) {
+#pragma clang fp contract(off)
+  constexpr int LPR = D / 8;
+  const int c8 = tid % LPR, rr = tid / LPR;
+  const int64_t t = s0 + rr;
+  const bool valid = t < n;
+  const int64_t tc = valid ? t : n - 1;  // clamped: the lanes of a token reduce together
+  f32x4 fr[4];
+  load_freqs<D>(prod.freqs, (int64_t)b * n + tc, c8, fr);
+  float wn[8];
+  load_w8(K ? prod.kw : prod.qw, c8, wn);
+  const uint16_t* row = prod.qkv + ((int64_t)b * n + tc) * (3LL * prod.h * D) + (K ? (int64_t)prod.h * D : 0) + c8 * 8;
+  const float qmax = (QK == kQK_INT8) ? kInt8Max : kFp8Max;
+  const int d0 = c8 * 8;
+  const int64_t frag = row_frag_offset(t, d0 / 32, (d0 / 16) & 1, D) + (d0 & 8);
+#pragma unroll
+  for (int it = 0; it < kSlabHeads / 4; ++it) {
+    const int hb = h0 + 4 * it;
+    if (hb >= h1) break;  // uniform
+    uint4 w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint4*>(row + (int64_t)min(hb + j, h1 - 1) * D);
+    const float r = tokens_rrms<D, 4>(w, prod.eps, tid);
+    float x[4][8], amax[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 y = valid ? rope8(w[j], quad_lane(r, j), wn, fr) : make_uint4(0, 0, 0, 0);
+      unpack8(y, x[j]);
+      if constexpr (K) {
+        // bf16(k - mean); rows past N stay zero
+        const f32x4* m4 = reinterpret_cast<const f32x4*>(mu + (min(hb + j, h1 - 1) - h0) * D + d0);
+        const f32x4 ma = m4[0], mb = m4[1];
+        const float m[8] = {ma[0], ma[1], ma[2], ma[3], mb[0], mb[1], mb[2], mb[3]};
+        const float keep = valid ? 1.0f : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const uint32_t p2 = pack_bf16x2(x[j][e] - m[e], x[j][e + 1] - m[e + 1]);  // round to nearest even
+          x[j][e] = __uint_as_float(p2 << 16) * keep;
+          x[j][e + 1] = __uint_as_float(p2 & 0xffff0000u) * keep;
+        }
+      }
+    }
+    row_amax<D, kGRAN_TOKEN, 4>(x, amax, nullptr);
+    // the division of head c8 % 4 in each lane, handed round the quad (store_rows)
+    const int mine = c8 & 3;
+    uint32_t amb = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) amb |= __float_as_uint(amax[j]) & (0u - (uint32_t)(mine == j));
+    const float am = __uint_as_float(amb);
+    const float inv_mine = qmax / fmaxf(am, kEps);  // IEEE division (correctly rounded)
+    const float scale_mine = (am / qmax) * fold;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float inv = quad_lane(inv_mine, j);
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = x[j][e] * inv;
+      uint2 word;
+      if (QK == kQK_INT8) {
+        word.x = pack_i8x4(y[0], y[1], y[2], y[3]);
+        word.y = pack_i8x4(y[4], y[5], y[6], y[7]);
+      } else {
+        word.x = pack_fp8x4(y[0], y[1], y[2], y[3]);
+        word.y = pack_fp8x4(y[4], y[5], y[6], y[7]);
+      }
+      if (hb + j < h1) {
+        const int64_t bh = (int64_t)b * prod.h + hb + j;
+        *reinterpret_cast<uint2*>(codes + bh * np * D + frag) = word;
+        if (c8 == j) scale[bh * np + t] = scale_mine;
+      }
+    }
+  }
+}
+
+// LDS of a K slab unit (byte offsets): the group's means float [kSlabHeads][D],
+// then head_mean's double [TPC][D] and chunk_colsum's double [4][D] for the
+// bounded-wait fallback.
+template <int D>
+struct SlabLds {
+  static constexpr int kMu = 0;
+  static constexpr int kMsum = kSlabHeads * D * 4;
+  static constexpr int kKsw = kMsum + (256 / D) * D * 8;
+  static constexpr int kTotal = kKsw + 4 * D * 8;
+};
+
 // One-kernel form with smoothing (not used under stream capture: the epoch is
 // a launch argument).  1D grid, units in dispatch order:
 //   [0, nsum)   K column sums of chunk u / BH of head u % BH; each publishes
@@ -900,22 +1074,38 @@ __device__ __forceinline__ double head_sum_part(bool ready, const HeadRows<D, PR
 // the workgroup forms the chunk sums itself, with the same arithmetic and
 // order (chunk_colsum), so every workgroup exits and the codes are the same
 // either way.
+// With the producer and per-token scales (SLAB) the Q and K roles are slab
+// units (slab_heads: one pass of RPP tokens for kSlabHeads heads) and the head means
+// are formed once: a column-sum unit that, after its own flag, finds every
+// chunk flag of its head set forms the mean (head_mean, the same sums in the
+// same order), stores it as fp32 [BH][D] beside the flags and publishes
+// mflag[head] = epoch.  Two units may both find it so and store the same
+// values; at least one does, because each reads the flags only after its own
+// flag store has completed.  Per row: the Q slab units of the block's passes
+// (pass-major, hg-head groups within), the block's V units, the K slab units
+// of block r - lag.  A K slab unit waits for its heads' mean flags (bounded,
+// with the chunk-sum fallback).
 template <int D, int QK, int PV, int GRAN, bool PROD>
-__global__ void __launch_bounds__(256) quantize_one_kernel(
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROD ? kProdWaves : 1))) quantize_one_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t bhn,
     int64_t n, int64_t np, float fold, double* __restrict__ ksum_part, uint64_t* __restrict__ flags,
-    uint64_t epoch, int spin_limit, int64_t lag, uint8_t* __restrict__ qc, float* __restrict__ qs, uint8_t* __restrict__ kc,
-    float* __restrict__ ks, uint8_t* __restrict__ vout, float* __restrict__ vs, uint16_t* __restrict__ kmean,
-    ProdArgs prod) {
+    uint64_t epoch, int spin_limit, int64_t lag, uint8_t* __restrict__ qc, float* __restrict__ qs,
+    uint8_t* __restrict__ kc, float* __restrict__ ks, uint8_t* __restrict__ vout, float* __restrict__ vs,
+    uint16_t* __restrict__ kmean, ProdArgs prod) {
   using L = QuantLds<D, PV>;
+  constexpr bool SLAB = PROD && GRAN == kGRAN_TOKEN;
   constexpr int TPC = 256 / D;
   constexpr int PASSES = 64 / (256 / (D / 8));
+  constexpr int RPP = 256 / (D / 8);
   static_assert(TPC * D * 8 + D * 4 + 4 * D * 8 <= L::kBytes, "K role scratch fits");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kTotal];
+  constexpr int kLdsBytes = (SLAB && SlabLds<D>::kTotal > L::kTotal) ? SlabLds<D>::kTotal : L::kTotal;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
   unsigned* blk_amax = reinterpret_cast<unsigned*>(lds + L::kAmax);
   const int tid = threadIdx.x;
   const int64_t nch = k_sum_chunks(n, D), nsum = nch * bhn;
   const int64_t nblk = np / 64;
+  uint64_t* mflags = flags + bhn * nch;                       // SLAB: [BH] mean flags
+  float* kmu = reinterpret_cast<float*>(mflags + bhn);        // SLAB: [BH][D] fp32 means
   int64_t u = blockIdx.x;
   if (u < nsum) {
     const int64_t ch = u / bhn;
@@ -933,92 +1123,201 @@ __global__ void __launch_bounds__(256) quantize_one_kernel(
     wait_vmem();
     __syncthreads();
     if (tid == 0) __hip_atomic_store(&flags[(int64_t)bh * nch + ch], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (SLAB) {
+      wait_vmem();  // this unit's flag is at the coherence point before the others are read
+      __syncthreads();
+      const uint64_t* hf = flags + (int64_t)bh * nch;
+      const uint64_t f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+      if (__syncthreads_and(f == epoch)) {
+        double mt[kMeanLoads];
+        load_chunk_sums<D, true>(ksum_part + (int64_t)bh * nch * D + tid % D, nch, tid, mt);
+        float* mu = reinterpret_cast<float*>(lds + TPC * D * 8);
+        head_mean<D>(mean_sum<D>(mt, nch, tid), n, reinterpret_cast<double(*)[D]>(lds), mu,
+                     kmean + (int64_t)bh * D, tid);
+        if (tid < D)
+          __hip_atomic_store(reinterpret_cast<uint32_t*>(kmu) + (int64_t)bh * D + tid, __float_as_uint(mu[tid]),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vmem();
+        __syncthreads();
+        if (tid == 0) __hip_atomic_store(&mflags[bh], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
     return;
   }
   u -= nsum;
-  // block roles with the K blocks `lag` rows behind the Q and V blocks
-  int role;
-  int64_t blk;
-  int bh;
-  const int64_t seg1 = 2 * bhn * lag, seg2 = 3 * bhn * (nblk - lag);
-  if (u < seg1) {
-    role = (int)(u & 1);
-    const int64_t rest = u >> 1;
-    blk = rest / bhn;
-    bh = (int)(rest - blk * bhn);
-  } else if (u < seg1 + seg2) {
-    const int64_t w = u - seg1;
-    role = (int)(w % 3);
-    const int64_t rest = w / 3;
-    const int64_t r = lag + rest / bhn;
-    bh = (int)(rest % bhn);
-    blk = role == 2 ? r - lag : r;
-  } else {
-    const int64_t w = u - seg1 - seg2;
-    role = 2;
-    blk = nblk - lag + w / bhn;
-    bh = (int)(w % bhn);
-  }
-  if (role != 2) {
-    const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
-    const int64_t tok0 = blk * 64;
-    if (role == 1) {
-      v_block<D, PV>(src.v, src.stride, tok0, n, blk, bh, np, vout, vs, lds, tid);
+  if constexpr (SLAB) {
+    // head groups: kSlabHeads consecutive heads of one batch, the last fewer
+    const int64_t ngb = (prod.h + kSlabHeads - 1) / kSlabHeads, ng = (bhn / prod.h) * ngb;
+    const int64_t per = PASSES * ng, per_qv = per + bhn;
+    const int64_t seg1 = per_qv * lag, seg2 = (per_qv + per) * (nblk - lag);
+    int64_t r, x;  // row, unit within the row
+    bool kunit = false;
+    if (u < seg1) {
+      r = u / per_qv;
+      x = u - r * per_qv;
+    } else if (u < seg1 + seg2) {
+      const int64_t w = u - seg1;
+      r = lag + w / (per_qv + per);
+      x = w % (per_qv + per);
+      if (x >= per_qv) {
+        kunit = true;
+        x -= per_qv;
+        r -= lag;
+      }
+    } else {
+      const int64_t w = u - seg1 - seg2;
+      r = nblk - lag + w / per;
+      x = w % per;
+      kunit = true;
+    }
+    if (!kunit && x >= per) {  // V of block r, one head
+      const int bh = (int)(x - per);
+      const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+      v_block<D, PV>(src.v, src.stride, r * 64, n, r, bh, np, vout, vs, lds, tid);
       return;
     }
-    if (GRAN == kGRAN_BLOCK64) {
-      if (tid == 0) *blk_amax = 0u;
-      __syncthreads();
+    const int64_t s0 = r * 64 + (x / ng) * RPP;  // the pass's first token
+    const int64_t g = x % ng;
+    const int b = (int)(g / ngb), h0 = (int)(g % ngb) * kSlabHeads;
+    const int h1 = min(h0 + kSlabHeads, prod.h);
+    if (!kunit) {
+      slab_heads<D, QK, false>(prod, b, h0, h1, s0, n, np, fold, nullptr, qc, qs, tid);
+      return;
     }
-    const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
-    rows_block<D, QK, GRAN, PROD>(src.q, src.stride, src.row0, prod.qw, prod, tok0, n, fold,
-                                  qc + (int64_t)bh * np * D, qs + sco, blk_amax, tid);
-    return;
-  }
-  // ---- K of one block ----
-  double(*msum)[D] = reinterpret_cast<double(*)[D]>(lds);
-  float* mu = reinterpret_cast<float*>(lds + TPC * D * 8);
-  double* ksw = reinterpret_cast<double*>(lds + TPC * D * 8 + D * 4);
-  const int64_t tok0 = blk * 64;
-  const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
-  const uint64_t* hf = flags + (int64_t)bh * nch;
-  // flags and sums are read with agent-scope relaxed atomic loads, which read
-  // the coherence point (sc1), issued only after the flags show this epoch
-  uint64_t f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
-  if (GRAN == kGRAN_BLOCK64 && tid == 0) *blk_amax = 0u;
-  bool ready = __syncthreads_and(f == epoch);
-  for (int r = 0; !ready && r < spin_limit; ++r) {
-    __builtin_amdgcn_s_sleep(32);
-    f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
-    ready = __syncthreads_and(f == epoch);
-  }
-  double s = 0.0;
-  if (ready) {
-    double mt[kMeanLoads];
-    load_chunk_sums<D, true>(ksum_part + (int64_t)bh * nch * D + tid % D, nch, tid, mt);
-    s = mean_sum<D>(mt, nch, tid);
-  } else {
-    // the chunk sums of this head, formed here in the same order
+    using S = SlabLds<D>;
+    float* mug = reinterpret_cast<float*>(lds + S::kMu);
+    double(*msum)[D] = reinterpret_cast<double(*)[D]>(lds + S::kMsum);
+    double* ksw = reinterpret_cast<double*>(lds + S::kKsw);
+    // the group's means, published by the column-sum units: one bounded wait
+    // for all their flags, then the rows; a head whose flag is still missing
+    // has its mean formed here from its chunk sums
+    const int cnt = h1 - h0;
+    const int64_t bh0 = (int64_t)b * prod.h + h0;
+    const uint32_t* kmu32 = reinterpret_cast<const uint32_t*>(kmu) + bh0 * D;
+    uint64_t f = tid < cnt ? __hip_atomic_load(&mflags[bh0 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+    bool ready = __syncthreads_and(f == epoch);
+    for (int it = 0; !ready && it < spin_limit; ++it) {
+      __builtin_amdgcn_s_sleep(32);
+      f = tid < cnt ? __hip_atomic_load(&mflags[bh0 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+      ready = __syncthreads_and(f == epoch);
+    }
+    if (ready) {
+      for (int i = tid; i < cnt * D; i += 256)
+        mug[i] = __uint_as_float(__hip_atomic_load(kmu32 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    } else {
 #pragma unroll 1
-    for (int64_t c = 0; c < nch; ++c) {
-      const double cs = chunk_colsum<D, PROD, 2>(src.k, src.stride, src.row0, prod, c, n, ksw, tid);
-      if (tid < D) msum[0][tid] = cs;  // chunk c's column sums
-      __syncthreads();
-      if (c % TPC == tid / D) s += msum[0][tid % D];
-      __syncthreads();
+      for (int j = 0; j < cnt; ++j) {
+        const uint64_t fj =
+            tid == 0 ? __hip_atomic_load(&mflags[bh0 + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+        if (__syncthreads_and(fj == epoch)) {
+          if (tid < D)
+            mug[j * D + tid] = __uint_as_float(
+                __hip_atomic_load(kmu32 + j * D + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          continue;
+        }
+        // the chunk sums of this head, formed here in the same order
+        const HeadRows<D, PROD> src(q, k, v, prod, (int)(bh0 + j), n);
+        double sj = 0.0;
+#pragma unroll 1
+        for (int64_t c = 0; c < nch; ++c) {
+          const double cs = chunk_colsum<D, PROD, 2>(src.k, src.stride, src.row0, prod, c, n, ksw, tid);
+          if (tid < D) msum[0][tid] = cs;  // chunk c's column sums
+          __syncthreads();
+          if (c % TPC == tid / D) sj += msum[0][tid % D];
+          __syncthreads();
+        }
+        head_mean<D>(sj, n, msum, mug + j * D, nullptr, tid);
+      }
     }
+    __syncthreads();
+    slab_heads<D, QK, true>(prod, b, h0, h1, s0, n, np, 1.0f, mug, kc, ks, tid);
+    return;
+  } else {
+    (void)mflags;
+    (void)kmu;
+    // block roles with the K blocks `lag` rows behind the Q and V blocks
+    int role;
+    int64_t blk;
+    int bh;
+    const int64_t seg1 = 2 * bhn * lag, seg2 = 3 * bhn * (nblk - lag);
+    if (u < seg1) {
+      role = (int)(u & 1);
+      const int64_t rest = u >> 1;
+      blk = rest / bhn;
+      bh = (int)(rest - blk * bhn);
+    } else if (u < seg1 + seg2) {
+      const int64_t w = u - seg1;
+      role = (int)(w % 3);
+      const int64_t rest = w / 3;
+      const int64_t r = lag + rest / bhn;
+      bh = (int)(rest % bhn);
+      blk = role == 2 ? r - lag : r;
+    } else {
+      const int64_t w = u - seg1 - seg2;
+      role = 2;
+      blk = nblk - lag + w / bhn;
+      bh = (int)(w % bhn);
+    }
+    if (role != 2) {
+      const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+      const int64_t tok0 = blk * 64;
+      if (role == 1) {
+        v_block<D, PV>(src.v, src.stride, tok0, n, blk, bh, np, vout, vs, lds, tid);
+        return;
+      }
+      if (GRAN == kGRAN_BLOCK64) {
+        if (tid == 0) *blk_amax = 0u;
+        __syncthreads();
+      }
+      const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+      rows_block<D, QK, GRAN, PROD>(src.q, src.stride, src.row0, prod.qw, prod, tok0, n, fold,
+                                    qc + (int64_t)bh * np * D, qs + sco, blk_amax, tid);
+      return;
+    }
+    // ---- K of one block ----
+    double(*msum)[D] = reinterpret_cast<double(*)[D]>(lds);
+    float* mu = reinterpret_cast<float*>(lds + TPC * D * 8);
+    double* ksw = reinterpret_cast<double*>(lds + TPC * D * 8 + D * 4);
+    const int64_t tok0 = blk * 64;
+    const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+    const uint64_t* hf = flags + (int64_t)bh * nch;
+    // flags and sums are read with agent-scope relaxed atomic loads, which read
+    // the coherence point (sc1), issued only after the flags show this epoch
+    uint64_t f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+    if (GRAN == kGRAN_BLOCK64 && tid == 0) *blk_amax = 0u;
+    bool ready = __syncthreads_and(f == epoch);
+    for (int r = 0; !ready && r < spin_limit; ++r) {
+      __builtin_amdgcn_s_sleep(32);
+      f = tid < nch ? __hip_atomic_load(&hf[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : epoch;
+      ready = __syncthreads_and(f == epoch);
+    }
+    double s = 0.0;
+    if (ready) {
+      double mt[kMeanLoads];
+      load_chunk_sums<D, true>(ksum_part + (int64_t)bh * nch * D + tid % D, nch, tid, mt);
+      s = mean_sum<D>(mt, nch, tid);
+    } else {
+      // the chunk sums of this head, formed here in the same order
+  #pragma unroll 1
+      for (int64_t c = 0; c < nch; ++c) {
+        const double cs = chunk_colsum<D, PROD, 2>(src.k, src.stride, src.row0, prod, c, n, ksw, tid);
+        if (tid < D) msum[0][tid] = cs;  // chunk c's column sums
+        __syncthreads();
+        if (c % TPC == tid / D) s += msum[0][tid % D];
+        __syncthreads();
+      }
+    }
+    uint4 w[PASSES];
+    rows_load<D>(src.k, src.stride, tok0, n, tid, w);  // after the mean: fewer registers live
+    head_mean<D>(s, n, msum, mu, blk == 0 ? kmean + (int64_t)bh * D : nullptr, tid);
+    const int64_t co = (int64_t)bh * np * D;
+    const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
+    const ProdRows pr{&prod, prod.kw, src.row0};
+    if (tok0 + 64 <= n)
+      rows_quant<D, QK, GRAN, PROD, false>(w, pr, tok0, n, 1.0f, mu, kc + co, ks + sco, blk_amax, tid);
+    else
+      rows_quant<D, QK, GRAN, PROD, true>(w, pr, tok0, n, 1.0f, mu, kc + co, ks + sco, blk_amax, tid);
   }
-  uint4 w[PASSES];
-  rows_load<D>(src.k, src.stride, tok0, n, tid, w);  // after the mean: fewer registers live
-  head_mean<D>(s, n, msum, mu, blk == 0 ? kmean + (int64_t)bh * D : nullptr, tid);
-  const int64_t co = (int64_t)bh * np * D;
-  const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
-  if (tok0 + 64 <= n)
-    rows_quant<D, QK, GRAN, PROD, false>(w, src.row0, prod.kw, prod, tok0, n, 1.0f, mu, kc + co, ks + sco, blk_amax,
-                                         tid);
-  else
-    rows_quant<D, QK, GRAN, PROD, true>(w, src.row0, prod.kw, prod, tok0, n, 1.0f, mu, kc + co, ks + sco, blk_amax,
-                                        tid);
 }
 
 // Single-read form with smoothing, for heads whose chunks are 256 tokens
@@ -1086,13 +1385,15 @@ __global__ void __launch_bounds__(256) quantize_fused_kernel(
       float kn[8];
       load_w8(prod.kw, c8, kn);
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < 4; ++b) {
+        const float r = tokens_rrms<D, PASSES>(w[b], prod.eps, tid);
 #pragma unroll
         for (int ps = 0; ps < PASSES; ++ps) {
           f32x4 fr[4];
           load_freqs<D>(prod.freqs, src.row0 + min(tok0 + 64 * b + rr + ps * RPP, n - 1), c8, fr);
-          w[b][ps] = rms_rope8<D>(w[b][ps], kn, fr, prod.eps);  // zero rows stay zero
+          w[b][ps] = rope8(w[b][ps], quad_lane(r, ps), kn, fr);  // zero rows stay zero
         }
+      }
     }
   };
   load_chunk();
@@ -1146,11 +1447,9 @@ __global__ void __launch_bounds__(256) quantize_fused_kernel(
     __builtin_amdgcn_sched_barrier(0);  // one block at a time
     if (t0 >= np) break;  // uniform: blocks past the padded length hold no codes
     if (t0 + 64 <= n)
-      rows_quant<D, QK, GRAN, false, false>(w[b], src.row0, prod.kw, prod, t0, n, 1.0f, mu, kc + co, ks + sco,
-                                            &blk_amax[b], tid);
+      rows_quant<D, QK, GRAN, false, false>(w[b], ProdRows{}, t0, n, 1.0f, mu, kc + co, ks + sco, &blk_amax[b], tid);
     else
-      rows_quant<D, QK, GRAN, false, true>(w[b], src.row0, prod.kw, prod, t0, n, 1.0f, mu, kc + co, ks + sco,
-                                           &blk_amax[b], tid);
+      rows_quant<D, QK, GRAN, false, true>(w[b], ProdRows{}, t0, n, 1.0f, mu, kc + co, ks + sco, &blk_amax[b], tid);
   }
 }
 
@@ -1189,11 +1488,11 @@ struct QuantCall {
   int path;  // kQuantAuto, kQuantTwoKernels, kQuantOneFallback, kQuantLagged
 };
 
-// A 64-bit value never passed to an earlier launch of this process: a clock
-// reading at first use (distinct across processes) plus a call counter.
-constexpr int64_t kLagUnits = 2048;  // Q and V workgroups dispatched ahead of the first K workgroup
+constexpr int64_t kLagUnits = 2048;  // Q and V head blocks dispatched ahead of the first K workgroup
 constexpr int64_t kFusedMinTokens = 1 << 18;  // head tokens (B * H * N) from which the single-read form runs
 
+// A 64-bit value never passed to an earlier launch of this process: a clock
+// reading at first use (distinct across processes) plus a call counter.
 uint64_t next_epoch() {
   static std::atomic<uint64_t> counter{0};
   static const uint64_t base =
@@ -1226,11 +1525,15 @@ hipError_t launch_quantize_t(const QuantCall& a, hipStream_t st) {
                            a.ks, a.vout, a.vs, a.kmean, a.prod);
         return hipGetLastError();
       }
-      const int64_t grid = nch * a.bh + 3 * nblk * a.bh;
+      constexpr bool SLAB = PROD && GRAN == kGRAN_TOKEN;
+      constexpr int PASSES = 64 / (256 / (D / 8));
+      // slab units: PASSES per block for each group of kSlabHeads heads of a batch
+      const int64_t groups = SLAB ? (a.bh / a.prod.h) * ((a.prod.h + kSlabHeads - 1) / kSlabHeads) : 0;
+      const int64_t grid = nch * a.bh + nblk * (SLAB ? a.bh + 2 * PASSES * groups : 3 * a.bh);
+      const int64_t lag = min(nblk, (kLagUnits + 2 * a.bh - 1) / (2 * a.bh));
       hipLaunchKernelGGL((quantize_one_kernel<D, QK, PV, GRAN, PROD>), dim3((unsigned)grid), dim3(256), 0, st, a.q,
-                         a.k, a.v, a.bh, a.n, np, a.fold, a.ws, flags, next_epoch(),
-                         a.path == kQuantOneFallback ? 0 : 4096, min(nblk, (kLagUnits + 2 * a.bh - 1) / (2 * a.bh)), a.qc, a.qs, a.kc, a.ks, a.vout, a.vs, a.kmean,
-                         a.prod);
+                         a.k, a.v, a.bh, a.n, np, a.fold, a.ws, flags, next_epoch(), spin, lag, a.qc, a.qs, a.kc,
+                         a.ks, a.vout, a.vs, a.kmean, a.prod);
       return hipGetLastError();
     }
   }
@@ -1278,7 +1581,9 @@ hipError_t launch_quantize(int qk, int pv, int gran, bool smooth, const uint16_t
 
 hipError_t launch_qkv_postprocess(const ProdArgs& prod, int64_t bh, int64_t n, int64_t d, uint16_t* q_out,
                                   uint16_t* k_out, uint16_t* v_out, hipStream_t st) {
-  const dim3 grid((unsigned)((n + 63) / 64 * bh));  // head fastest (block_coords)
+  const int64_t rpp = 256 / (d / 8);  // tokens per slab
+  const int64_t groups = (prod.h + kSlabHeads - 1) / kSlabHeads;
+  const dim3 grid((unsigned)((bh / prod.h) * ((n + rpp - 1) / rpp) * groups));
   if (d == 128)
     hipLaunchKernelGGL(qkv_postprocess_kernel<128>, grid, dim3(256), 0, st, prod, n, q_out, k_out, v_out);
   else if (d == 64)
@@ -1307,10 +1612,12 @@ int64_t quant_grid_units(int64_t bh, int64_t n, int64_t d) {
 }
 
 // fp64 column sums of K per head and chunk, [bh][nch][d], then the chunks'
-// flags of the one-kernel form, uint64 [bh][nch].
+// flags of the one-kernel form, uint64 [bh][nch], then (its producer form)
+// the heads' mean flags, uint64 [bh], and means, fp32 [bh][d].
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d) {
   const int64_t nch = k_sum_chunks(n, d);
-  return (size_t)(bh * nch * d) * sizeof(double) + (size_t)(bh * nch) * sizeof(uint64_t);
+  return (size_t)(bh * nch * d) * sizeof(double) + (size_t)(bh * nch + bh) * sizeof(uint64_t) +
+         (size_t)(bh * d) * sizeof(float);
 }
 
 }  // namespace sage

@@ -85,10 +85,12 @@ const char* sage_last_error(void);
 /* Np for a sequence length: N rounded up to a multiple of 128. */
 int64_t sage_padded_len(int64_t n);
 
-/* Bytes of device workspace sage_quantize_qkv needs when smoothing: fp64
- * column sums of K per head and 256-token chunk, [bh][ceil(n/256)][d]
- * (written, then read, by the call; no prior contents needed).  16-byte
- * aligned.  Concurrent calls need separate workspaces. */
+/* Bytes of device workspace sage_quantize_qkv and sage_quantize_from_qkv
+ * need when smoothing: fp64 column sums of K per head and 256-token chunk,
+ * [bh][ceil(n/256)][d], an 8-byte flag per chunk, and per head an 8-byte
+ * flag and the fp32 mean of K (written, then read, by the call; no prior
+ * contents needed).  16-byte aligned.  Concurrent calls need separate
+ * workspaces. */
 size_t sage_quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
 
 /* K smoothing + Q/K (and, for fp8 PV, V) quantization.

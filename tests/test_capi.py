@@ -51,15 +51,18 @@ def test_sizes_and_padding():
     from futudiffu_amd import _lib
     lib = _lib.load()
     assert [lib.sage_padded_len(n) for n in (1, 128, 129, 4416)] == [128, 128, 256, 4480]
-    # fp64 K column sums per head and chunk, then an 8-byte flag per chunk;
-    # chunks of 256 tokens, widened by multiples of 256 so that a head has at
-    # most 12 * (256 / D) of them
-    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == 30 * 18 * (128 + 1) * 8
-    assert lib.sage_quant_workspace_bytes(2, 256, 64) == 2 * 1 * (64 + 1) * 8
-    assert lib.sage_quant_workspace_bytes(1, 257, 64) == 2 * (64 + 1) * 8
+    # fp64 K column sums per head and chunk, then an 8-byte flag per chunk,
+    # then per head an 8-byte mean flag and the fp32 mean; chunks of 256
+    # tokens, widened by multiples of 256 so that a head has at most
+    # 12 * (256 / D) of them
+    def ws(bh, nch, d):
+        return bh * nch * (d + 1) * 8 + bh * (8 + 4 * d)
+    assert lib.sage_quant_workspace_bytes(30, 4416, 128) == ws(30, 18, 128)
+    assert lib.sage_quant_workspace_bytes(2, 256, 64) == ws(2, 1, 64)
+    assert lib.sage_quant_workspace_bytes(1, 257, 64) == ws(1, 2, 64)
     # 20000 tokens: 79 pieces of 256 -> 1024-token chunks (20) at D=128, 512-token (40) at D=64
-    assert lib.sage_quant_workspace_bytes(1, 20000, 128) == 20 * (128 + 1) * 8
-    assert lib.sage_quant_workspace_bytes(1, 20000, 64) == 40 * (64 + 1) * 8
+    assert lib.sage_quant_workspace_bytes(1, 20000, 128) == ws(1, 20, 128)
+    assert lib.sage_quant_workspace_bytes(1, 20000, 64) == ws(1, 40, 64)
     # per-batch summaries of every 64-key tile and 32- and 128-row query block
     # and the scheduled key-tile range of each 128-row query block (int4 each),
     # the list of split query tiles (a count and 2 entries, int4 each),
