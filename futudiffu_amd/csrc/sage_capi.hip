@@ -72,7 +72,8 @@ size_t sage_attn_masked_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t
 namespace {
 
 // Outputs and workspace of a quantization call.
-int check_quant_outputs(int64_t bh, int64_t n, int64_t d, int pv_kind, int smooth_k, const void* q_codes,
+int check_quant_outputs(int64_t bh, int64_t n, int64_t d, int64_t h_producer, int pv_kind, int smooth_k,
+                        const void* q_codes,
                         const float* q_scale, const void* k_codes, const float* k_scale, const void* v_out,
                         const float* v_scale, const void* k_mean, const void* workspace, size_t workspace_bytes) {
   if (!q_codes || !q_scale || !k_codes || !k_scale || !v_out) return fail(SAGE_ERR_ARG, "null tensor pointer");
@@ -81,9 +82,10 @@ int check_quant_outputs(int64_t bh, int64_t n, int64_t d, int pv_kind, int smoot
   for (const void* p : ptrs)
     if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
   if (v_scale && !aligned16(v_scale)) return fail(SAGE_ERR_ALIGN, "v_scale must be 16-byte aligned");
-  if (sage::quant_grid_units(bh, n, d) > kMaxGridUnits)
+  const int64_t units = sage::quant_grid_units(bh, n, d, h_producer);
+  if (units > kMaxGridUnits)
     return fail(SAGE_ERR_ARG, "quantizing bh=%lld x n=%lld takes %lld workgroups, beyond one launch's %lld",
-                (long long)bh, (long long)n, (long long)sage::quant_grid_units(bh, n, d), (long long)kMaxGridUnits);
+                (long long)bh, (long long)n, (long long)units, (long long)kMaxGridUnits);
   if (smooth_k) {
     if (!k_mean) return fail(SAGE_ERR_ARG, "smooth_k needs k_mean");
     const size_t need = sage::quant_workspace_bytes(bh, n, d);
@@ -107,9 +109,14 @@ int check_producer(const void* qkv, const float* q_norm_w, const float* k_norm_w
   for (const void* p : ptrs)
     if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
   if (!(norm_eps >= 0.0f)) return fail(SAGE_ERR_ARG, "norm_eps must be >= 0");
-  // one workgroup per (64-token block, head) in a 1D grid
+  // the producer's backward: one workgroup per (64-token block, head) in a 1D grid
   if (b * h * ((n + 63) / 64) > kMaxGridUnits)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/64) = %lld exceeds the grid limit", (long long)(b * h * ((n + 63) / 64)));
+  // the standalone producer: one per (pass of 256/(d/8) tokens, group of kSlabHeads heads)
+  const int64_t rpp = 256 / (d / 8);
+  const int64_t slabs = b * ((n + rpp - 1) / rpp) * ((h + sage::kSlabHeads - 1) / sage::kSlabHeads);
+  if (slabs > kMaxGridUnits)
+    return fail(SAGE_ERR_ARG, "%lld producer slabs exceed the grid limit", (long long)slabs);
   // 256 token rows of the projection output (3*h*d bf16 each) within 32-bit byte offsets
   if (3 * h * d * 2 * 256 > (int64_t)0xffffffff)
     return fail(SAGE_ERR_ARG, "3*h*d = %lld channels per token row is too wide for the producer", (long long)(3 * h * d));
@@ -165,7 +172,7 @@ int sage_quantize_qkv(const void* q, const void* k, const void* v, int64_t bh, i
   const void* ins[] = {q, k, v};
   for (const void* p : ins)
     if (!aligned16(p)) return fail(SAGE_ERR_ALIGN, "tensor pointers must be 16-byte aligned");
-  st = check_quant_outputs(bh, n, d, pv_kind, smooth_k, q_codes, q_scale, k_codes, k_scale, v_out, v_scale, k_mean,
+  st = check_quant_outputs(bh, n, d, 0, pv_kind, smooth_k, q_codes, q_scale, k_codes, k_scale, v_out, v_scale, k_mean,
                            workspace, workspace_bytes);
   if (st) return st;
   hipError_t e = sage::launch_quantize(
@@ -219,7 +226,7 @@ int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* 
   if (st) return st;
   st = check_common(b * h, n, d, qk_kind, pv_kind, granularity);
   if (st) return st;
-  st = check_quant_outputs(b * h, n, d, pv_kind, smooth_k, q_codes, q_scale, k_codes, k_scale, v_out, v_scale,
+  st = check_quant_outputs(b * h, n, d, h, pv_kind, smooth_k, q_codes, q_scale, k_codes, k_scale, v_out, v_scale,
                            k_mean, workspace, workspace_bytes);
   if (st) return st;
   hipError_t e = sage::launch_quantize(
@@ -446,7 +453,7 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
   // the dK/dV and dQ launches: 512-thread workgroups, one per 128-row tile
   if ((b * h) * ((n + 127) / 128) > kMaxGridUnits / 2)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(b * h * ((n + 127) / 128)));
-  if (sage::quant_grid_units(b * h, n, d) > kMaxGridUnits)
+  if (sage::quant_grid_units(b * h, n, d, 0) > kMaxGridUnits)
     return fail(SAGE_ERR_ARG, "quantizing b*h=%lld x n=%lld exceeds one launch's %lld workgroups", (long long)(b * h),
                 (long long)n, (long long)kMaxGridUnits);
   const BwdWorkspace ws = bwd_workspace(b, b * h, n, d);

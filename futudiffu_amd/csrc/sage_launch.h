@@ -112,6 +112,10 @@ inline TailSplit tail_split(int64_t n_items, int64_t nt) {
 // transpose, fused_kernels.py:271-390).  With qkv set, the quantization reads
 // the projection output and applies the producer itself; with qkv null it
 // reads bf16 q, k, v [BH, N, D].
+// Heads per slab unit of the producer kernels (one pass of tokens for this
+// many heads of a batch in one workgroup).
+constexpr int kSlabHeads = 8;
+
 struct ProdArgs {
   const uint16_t* qkv;  // bf16 [B, N, 3*H*D]
   const float* qw;      // RMSNorm weights of q and k, fp32 [D]
@@ -133,7 +137,7 @@ hipError_t launch_qkv_postprocess(const ProdArgs& prod, int64_t bh, int64_t n, i
 hipError_t launch_qkv_postprocess_bwd(const ProdArgs& prod, int64_t bh, int64_t n, int64_t d, const uint16_t* gq,
                                       const uint16_t* gk, const uint16_t* gv, uint16_t* dqkv, hipStream_t st);
 size_t quant_workspace_bytes(int64_t bh, int64_t n, int64_t d);
-int64_t quant_grid_units(int64_t bh, int64_t n, int64_t d);
+int64_t quant_grid_units(int64_t bh, int64_t n, int64_t d, int64_t h_producer);
 
 hipError_t launch_attn(int qk, int pv, int gran, int mask, const AttnParams& p, int64_t d, int nb, hipStream_t st);
 // Per-batch document-id summaries (min doc, max doc, #valid, #padding) of every

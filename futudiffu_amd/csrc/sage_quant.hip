@@ -151,12 +151,12 @@ __device__ __forceinline__ void row_amax(const float (&x)[PASSES][8], float (&am
 
 // ---- q/k producer (fused_qkv_postprocess, fused_kernels.py:271-390) ---------
 
-// Heads per slab unit: a workgroup that takes one pass of tokens for this many
-// heads of a batch (the last group of a batch may have fewer) loads the
-// tokens' rotation rows once for all of them.  The rotations are 16 bytes per
-// channel pair and token, four times the bf16 data of a head; read per head
-// they made up most of the L2 traffic of the producer-fused quantization.
-constexpr int kSlabHeads = 8;
+// Slab units (kSlabHeads, sage_launch.h): a workgroup that takes one pass of
+// tokens for kSlabHeads heads of a batch (the last group of a batch may have
+// fewer) loads the tokens' rotation rows once for all of them.  The rotations
+// are 16 bytes per channel pair and token, four times the bf16 data of a
+// head; read per head they made up most of the L2 traffic of the
+// producer-fused quantization.
 
 // Sum over the LPR consecutive lanes (8 or 16) that hold one token's channels:
 // a pairwise tree over the lanes in order, with DPP moves of the two halves of
@@ -1606,9 +1606,15 @@ hipError_t launch_qkv_postprocess_bwd(const ProdArgs& prod, int64_t bh, int64_t 
 }
 
 // Workgroups of the largest quantization launch: the column-sum chunks plus
-// three roles per 64-token block, for every head.
-int64_t quant_grid_units(int64_t bh, int64_t n, int64_t d) {
-  return (k_sum_chunks(n, d) + 3 * (padded_len(n) / 64)) * bh;
+// three roles per 64-token block, for every head; with the producer (h > 0
+// heads per batch) also the slab form's chunks, V blocks and two slab units
+// per pass of a block for each group of kSlabHeads heads.
+int64_t quant_grid_units(int64_t bh, int64_t n, int64_t d, int64_t h) {
+  const int64_t nch = k_sum_chunks(n, d), nblk = padded_len(n) / 64;
+  const int64_t plain = (nch + 3 * nblk) * bh;
+  if (h <= 0) return plain;
+  const int64_t groups = (bh / h) * ((h + kSlabHeads - 1) / kSlabHeads), passes = d / 32;
+  return std::max(plain, nch * bh + nblk * (bh + 2 * passes * groups));
 }
 
 // fp64 column sums of K per head and chunk, [bh][nch][d], then the chunks'
