@@ -35,10 +35,11 @@ def _inputs(b, n, h, d, seed):
     return qkv, qw, kw, freqs
 
 
-# head counts around the 8-head slab groups: one group of 2 or 3, 8 + 1 and
-# 8 + 4 heads per batch over several batches, and 8, 8, 8, 6 at full size
+# head counts around the 8-head slab groups: one group of 1, 2 or 3, 8 + 1 and
+# 8 + 4 heads per batch over several batches, and 8, 8, 8, 6 at full size;
+# single-token and sub-pass sequences
 @pytest.mark.parametrize("B,N,H,D", [(2, 300, 3, 128), (1, 77, 2, 64), (2, 300, 9, 128), (3, 129, 12, 64),
-                                     (1, 4416, 30, 128)])
+                                     (3, 1, 1, 64), (2, 17, 5, 128), (1, 4416, 30, 128)])
 def test_qkv_postprocess_matches_oracle(cuda, B, N, H, D):
     from futudiffu_amd import sage_attention as SA
     qkv, qw, kw, freqs = _inputs(B, N, H, D, seed=N + D)
@@ -66,7 +67,8 @@ def _same_quantized(a, b):
 
 
 @pytest.mark.parametrize("qk,pv,gran,smooth", VARIANTS)
-@pytest.mark.parametrize("B,N,H,D", [(2, 300, 3, 128), (1, 700, 2, 64), (2, 300, 9, 128), (3, 129, 12, 64)])
+@pytest.mark.parametrize("B,N,H,D", [(2, 300, 3, 128), (1, 700, 2, 64), (2, 300, 9, 128), (3, 129, 12, 64),
+                                     (3, 1, 1, 64), (2, 17, 5, 128)])
 def test_quantize_from_qkv_equals_two_steps(cuda, B, N, H, D, qk, pv, gran, smooth):
     from futudiffu_amd import sage_attention as SA
     qkv, qw, kw, freqs = (t.to(cuda) for t in _inputs(B, N, H, D, seed=11 + N))
