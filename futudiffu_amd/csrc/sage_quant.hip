@@ -1322,7 +1322,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROD ?
 
 // Single-read form with smoothing, for heads whose chunks are 256 tokens
 // (k_sum_tokens(n, D) == 256; not used under stream capture, nor with the
-// producer, whose K units would hold too many registers).  1D grid, head
+// producer, whose K units would hold too many registers; prod is unused).  1D grid, head
 // after head: the head's nch K units, then its 2 * nblk Q and V block units.
 // A K unit loads its 256 tokens once into registers (four 64-token blocks in
 // the lane layout of rows_load), adds their fp64 column sums in chunk_colsum's
@@ -1333,7 +1333,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROD ?
 // a head's K units are consecutive in dispatch order, so every unit a waiting
 // one depends on is dispatched before any later head's work, and the bounded
 // wait covers the rest.
-template <int D, int QK, int PV, int GRAN, bool PROD>
+template <int D, int QK, int PV, int GRAN>
 __global__ void __launch_bounds__(256) quantize_fused_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t bhn,
     int64_t n, int64_t np, float fold, double* __restrict__ ksum_part, uint64_t* __restrict__ flags,
@@ -1354,7 +1354,7 @@ __global__ void __launch_bounds__(256) quantize_fused_kernel(
   const int64_t per_head = nch + 2 * nblk;
   const int bh = (int)(blockIdx.x / per_head);
   const int64_t u = blockIdx.x - (int64_t)bh * per_head;
-  const HeadRows<D, PROD> src(q, k, v, prod, bh, n);
+  const HeadRows<D, false> src(q, k, v, prod, bh, n);
   if (u >= nch) {
     const int role = (int)((u - nch) & 1);
     const int64_t blk = (u - nch) >> 1;
@@ -1368,7 +1368,7 @@ __global__ void __launch_bounds__(256) quantize_fused_kernel(
       __syncthreads();
     }
     const int64_t sco = (GRAN == kGRAN_TOKEN) ? (int64_t)bh * np : (int64_t)bh * (np / 64);
-    rows_block<D, QK, GRAN, PROD>(src.q, src.stride, src.row0, prod.qw, prod, tok0, n, fold,
+    rows_block<D, QK, GRAN, false>(src.q, src.stride, src.row0, prod.qw, prod, tok0, n, fold,
                                   qc + (int64_t)bh * np * D, qs + sco, blk_amax, tid);
     return;
   }
@@ -1377,24 +1377,10 @@ __global__ void __launch_bounds__(256) quantize_fused_kernel(
   const int64_t tok0 = ch * 256;
   const int wave = tid >> 6, c8 = tid % LPR, rr = tid / LPR;
   uint4 w[4][PASSES];
-  // the chunk's 256 tokens (through the producer for PROD)
+  // the chunk's 256 tokens
   auto load_chunk = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) rows_load<D>(src.k, src.stride, tok0 + 64 * b, n, tid, w[b]);
-    if constexpr (PROD) {
-      float kn[8];
-      load_w8(prod.kw, c8, kn);
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float r = tokens_rrms<D, PASSES>(w[b], prod.eps, tid);
-#pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-          f32x4 fr[4];
-          load_freqs<D>(prod.freqs, src.row0 + min(tok0 + 64 * b + rr + ps * RPP, n - 1), c8, fr);
-          w[b][ps] = rope8(w[b][ps], quad_lane(r, ps), kn, fr);  // zero rows stay zero
-        }
-      }
-    }
   };
   load_chunk();
   if (GRAN == kGRAN_BLOCK64 && tid < 4) blk_amax[tid] = 0u;
@@ -1434,7 +1420,7 @@ __global__ void __launch_bounds__(256) quantize_fused_kernel(
     if (tid == 0) __hip_atomic_store(&flags[(int64_t)bh * nch + ch], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const bool ready = wait_head_flags(flags + (int64_t)bh * nch, nch, epoch, spin_limit, tid);
-  const double s = head_sum_part<D, PROD>(ready, src, prod, bh, n, nch, ksum_part, lds, tid);
+  const double s = head_sum_part<D, false>(ready, src, prod, bh, n, nch, ksum_part, lds, tid);
   if (!ready) load_chunk();  // (rare) the tokens again: none stay in registers while the sums are formed
   head_mean<D>(s, n, reinterpret_cast<double(*)[D]>(lds), reinterpret_cast<float*>(lds + TPC * D * 8),
                ch == 0 ? kmean + (int64_t)bh * D : nullptr, tid);
@@ -1516,14 +1502,16 @@ hipError_t launch_quantize_t(const QuantCall& a, hipStream_t st) {
       // tokens (measured: 4 x 30 x 4352 x 128 135.0 -> 118.8 us; at 30 x
       // 4416 its halved occupancy and each K unit's serial wait make it slower,
       // 31.3 -> 37.5 us), when a head's chunks are 256 tokens
-      const bool fits = !PROD && k_sum_tokens(a.n, D) == 256;
-      const bool big = a.bh * a.n >= kFusedMinTokens;
-      if (fits && (a.path == kQuantFused || (a.path != kQuantLagged && big))) {
-        const int64_t grid = a.bh * (nch + 2 * nblk);
-        hipLaunchKernelGGL((quantize_fused_kernel<D, QK, PV, GRAN, PROD>), dim3((unsigned)grid), dim3(256), 0, st,
-                           a.q, a.k, a.v, a.bh, a.n, np, a.fold, a.ws, flags, next_epoch(), spin, a.qc, a.qs, a.kc,
-                           a.ks, a.vout, a.vs, a.kmean, a.prod);
-        return hipGetLastError();
+      if constexpr (!PROD) {
+        const bool fits = k_sum_tokens(a.n, D) == 256;
+        const bool big = a.bh * a.n >= kFusedMinTokens;
+        if (fits && (a.path == kQuantFused || (a.path != kQuantLagged && big))) {
+          const int64_t grid = a.bh * (nch + 2 * nblk);
+          hipLaunchKernelGGL((quantize_fused_kernel<D, QK, PV, GRAN>), dim3((unsigned)grid), dim3(256), 0, st,
+                             a.q, a.k, a.v, a.bh, a.n, np, a.fold, a.ws, flags, next_epoch(), spin, a.qc, a.qs,
+                             a.kc, a.ks, a.vout, a.vs, a.kmean, a.prod);
+          return hipGetLastError();
+        }
       }
       constexpr bool SLAB = PROD && GRAN == kGRAN_TOKEN;
       constexpr int PASSES = 64 / (256 / (D / 8));
