@@ -8,7 +8,8 @@ tracing under gradient checkpointing and torch.compile work
 
 * each forward op is captured in a HIP graph (torch.cuda.CUDAGraph) and
   replayed on three new inputs, with eager calls and synchronizations between
-  the replays; every replay must equal the eager call bit for bit;
+  the replays; every replay must equal the eager call bit for bit (the
+  producer op too, whose quantization takes another form under capture);
 * torch.library.opcheck runs on every forward and backward op (schema, fake
   tensor, autograd registration, AOT dispatch);
 * a gradient-checkpointed block that calls futudiffu_ii::sage_attn_masked
@@ -131,6 +132,32 @@ def test_graph_capture_sage_attn_ext_doc_ids(cuda):
         return torch.ops.futudiffu_ii.sage_attn_ext(q, k, v, None, doc, sc, "int8", "fp8", "token", True, "bhnd")
 
     _capture_and_replay(cuda, fn, make, "sage_attn_ext")
+
+
+def test_graph_capture_sage_attn_qkv_masked(cuda):
+    """futudiffu_ii::sage_attn_qkv_masked from the QKV projection output
+    (1x1000x(3*12*128), tile mask): under capture the quantization takes its
+    two-kernel form, eagerly the one-kernel slab form; every replay must equal
+    the eager call bit for bit."""
+    B, N, H, D = 1, 1000, 12, 128
+    bm = O.build_block_mask([300, 500, 200], N).to(cuda)
+    sc = 1.0 / math.sqrt(D)
+    g = torch.Generator().manual_seed(270)
+    qw = (1.0 + 0.3 * torch.randn(D, generator=g)).to(cuda)
+    kw = (1.0 + 0.3 * torch.randn(D, generator=g)).to(cuda)
+    ang = torch.rand(B, N, 1, D // 2, generator=g) * 6.283
+    c, s = torch.cos(ang), torch.sin(ang)
+    freqs = torch.stack([torch.stack([c, -s], -1), torch.stack([s, c], -1)], -2).to(cuda)
+    print("graph capture: futudiffu_ii::sage_attn_qkv_masked 1x1000x12x128 (tile mask)", flush=True)
+
+    def make(i):
+        gi = torch.Generator().manual_seed(271 + i)
+        return ((torch.randn(B, N, 3 * H * D, generator=gi) * 2.0).bfloat16().to(cuda),)
+
+    def fn(qkv):
+        return torch.ops.futudiffu_ii.sage_attn_qkv_masked(qkv, qw, kw, freqs, bm, H, D, 1e-6, sc)
+
+    _capture_and_replay(cuda, fn, make, "sage_attn_qkv_masked")
 
 
 def _opcheck(op, args, what):
