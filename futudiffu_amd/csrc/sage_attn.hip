@@ -1174,6 +1174,119 @@ __device__ __forceinline__ void store_partial(float* slot, const f32x16* o, floa
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_acc), rs, tid * 4, (128 * D + 256) * 4, 0);
 }
 
+// store_partial for the in-kernel merge: the same layout, written through to
+// the device's coherence point by agent-scope relaxed atomic stores (sc1 on
+// gfx950), so that the merging workgroup, on any XCD, reads it there once the
+// writer's stores have completed.
+template <int D>
+__device__ __forceinline__ void store_partial_coherent(float* slot, const f32x16* o, float m_ref, float l_acc) {
+  constexpr int NC = D / 32;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  uint32_t* s32 = reinterpret_cast<uint32_t*>(slot) + wave * NC * 16 * 64 + lane;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      __hip_atomic_store(s32 + (c * 16 + e) * 64, __float_as_uint(o[c][e]), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t* tail = reinterpret_cast<uint32_t*>(slot) + 128 * D;
+  __hip_atomic_store(tail + tid, __float_as_uint(m_ref), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(tail + 256 + tid, __float_as_uint(l_acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Counts a piece's arrival at its split item (AttnParams::merge_ctr); true
+// for the last of `parts` pieces.  A counter whose tag is not this launch's
+// (another call's, or memory never written) starts again from 0.
+__device__ __forceinline__ bool arrive_last(uint64_t* ctr, uint64_t tag, int parts) {
+  const uint64_t mine = tag << 8;
+  uint64_t old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t next;
+  do {
+    next = ((old & ~(uint64_t)0xff) == mine ? old : mine) + 1;
+  } while (!__hip_atomic_compare_exchange_weak(ctr, &old, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT));
+  return (int)(next & 0xff) == parts;
+}
+
+// The merge of split item si by the workgroup of its last piece, with the
+// operations of merge_split_kernel in the same order (so the same bits).  The
+// partials are read by agent-scope relaxed atomic loads (sc1), issued after
+// this piece's arrival was counted behind every other piece's, whose stores
+// had completed before they counted.  fac: LDS [8][128] floats.
+template <int D>
+__device__ __forceinline__ void merge_pieces(const AttnParams& p, int64_t si, float* fac) {
+  constexpr int NC = D / 32;
+  constexpr int kMaxParts = 8;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, h = lane >> 5, r = lane & 31;
+  const int parts = p.split_parts;
+  const int nq = (int)(p.np / kRowsPerWG);
+  const int64_t pos = p.n_whole + si;
+  const int bh = (int)(pos / nq), qt = (int)(pos % nq);
+  const int64_t q0 = (int64_t)qt * kRowsPerWG + 32 * w;
+  const uint32_t* slots = reinterpret_cast<const uint32_t*>(p.part + si * parts * kPartFloats<D>);
+  auto ld = [](const uint32_t* a) __attribute__((always_inline)) {
+    return __uint_as_float(__hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  };
+  if (lane < 32) {  // the factors of row `lane` of this wave's 32 rows
+    const int row = lane;
+    float m[kMaxParts], l[kMaxParts];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q) {
+      if (q < parts) {
+        const uint32_t* sl = slots + q * kPartFloats<D> + 128 * D;
+        m[q] = ld(sl + w * 64 + row);
+        l[q] = ld(sl + 256 + w * 64 + row) + ld(sl + 256 + w * 64 + 32 + row);
+        mx = fmaxf(mx, m[q]);
+      }
+    }
+    float tot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q) {
+      if (q < parts) {
+        m[q] = m[q] > -INFINITY ? __builtin_amdgcn_exp2f(m[q] - mx) : 0.0f;
+        tot = fmaf(m[q], l[q], tot);
+      }
+    }
+    const bool empty = !(tot > 0.0f);
+    const float inv = empty ? 0.0f : 1.0f / tot;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q)
+      if (q < parts) fac[q * 128 + w * 32 + row] = m[q] * inv;
+    if (q0 + row < p.n) p.lse[(int64_t)bh * p.n + q0 + row] = empty ? -INFINITY : (mx + log2f(tot));
+  }
+  __syncthreads();
+  // lane (h, r) holds channel 32c + r of rows 8j + 4h + i (element 4j + i of chunk c)
+  float acc[NC][16];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[c][e] = 0.0f;
+#pragma unroll 1
+  for (int q = 0; q < parts; ++q) {
+    const uint32_t* s = slots + q * kPartFloats<D> + w * NC * 16 * 64 + lane;
+    float x[NC][16];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[c][e] = ld(s + (c * 16 + e) * 64);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[c][e] = fmaf(fac[q * 128 + w * 32 + 8 * (e / 4) + 4 * h + (e % 4)], x[c][e], acc[c][e]);
+  }
+  const int bh_b = bh / p.h, bh_h = bh - bh_b * p.h;
+  uint16_t* ob = p.out + bh_b * p.out_bs + bh_h * p.out_hs + q0 * p.out_rs + r;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = 8 * (e / 4) + 4 * h + (e % 4);
+      if (q0 + row < p.n) ob[row * p.out_rs + 32 * c] = f32_to_bf16_rne(acc[c][e]);
+    }
+}
+
 template <int D, int QK, int PV, int GRAN, int MASK, bool DUMP = false>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
   using SM = Smem<D, PV>;
@@ -1190,18 +1303,34 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnParams p) {
     // items, dealt to XCDs (workgroup i runs on XCD i % 8) in contiguous
     // ranges so that an XCD's resident workgroups share K/V tiles in its L2.
     // Later workgroups, dispatched last, take the pieces of the split items
-    // and leave partials for merge_split_kernel.
+    // and leave partials; the last piece of an item to arrive merges them
+    // (merge_pieces), or merge_split_kernel does after the launch.
     const int64_t b = blockIdx.x;
     if (b >= p.n_whole) {
       const int64_t c = b - p.n_whole;
-      const int64_t pos = p.n_whole + c / p.split_parts;
+      const int64_t si = c / p.split_parts;
+      const int64_t pos = p.n_whole + si;
       const int part = (int)(c % p.split_parts);
       bh = (int)(pos / nq);
       qt = (int)(pos % nq);
       const int t0 = (int)((int64_t)part * p.nt / p.split_parts);
       const int t1 = (int)((int64_t)(part + 1) * p.nt / p.split_parts);
       item_tiles<D, QK, PV, GRAN, 0, DUMP>(p, smem, bh, qt, t0, t1, o, m_ref, l_acc);
-      store_partial<D>(p.part + c * kPartFloats<D>, o, m_ref, l_acc);
+      if (p.merge_ctr == nullptr) {
+        store_partial<D>(p.part + c * kPartFloats<D>, o, m_ref, l_acc);
+        return;
+      }
+      store_partial_coherent<D>(p.part + c * kPartFloats<D>, o, m_ref, l_acc);
+      wait_vmem();  // this piece's partial is at the coherence point before it counts
+      __syncthreads();
+      int* last = reinterpret_cast<int*>(smem);
+      if (threadIdx.x == 0) *last = arrive_last(p.merge_ctr + si, p.merge_tag, p.split_parts) ? 1 : 0;
+      __syncthreads();
+      if (*last == 0) return;
+      __syncthreads();  // every wave has read the decision before the factors reuse the LDS
+      merge_pieces<D>(p, si, reinterpret_cast<float*>(smem));
+      if (threadIdx.x == 0)
+        __hip_atomic_store(p.merge_ctr + si, p.merge_tag << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
     const int x = (int)(b % 8);
@@ -1327,7 +1456,7 @@ hipError_t launch_attn_g(int mask, const AttnParams& p, hipStream_t st) {
     case 2: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 2>), grid, dim3(256), 0, st, p); break;
     case 3: hipLaunchKernelGGL((attn_fwd_kernel<D, QK, PV, GRAN, 3>), grid, dim3(256), 0, st, p); break;
   }
-  if (n_split > 0)
+  if (n_split > 0 && p.merge_ctr == nullptr)
     hipLaunchKernelGGL(merge_split_kernel<D>, dim3((unsigned)n_split, 4, 4), dim3(256), 0, st, p);
   return hipGetLastError();
 }
@@ -1463,8 +1592,11 @@ AttnWorkspace attn_workspace(int64_t b, int64_t h, int64_t n, int64_t d, bool ma
   // list of split query tiles (a count and kHeavyMax entries)
   w.heavy_off = (size_t)(b * (nt + np / 32 + np / 128 + np / 128)) * sizeof(int4);
   w.part_off = (w.heavy_off + (size_t)(1 + kHeavyMax) * sizeof(int4) + 255) & ~(size_t)255;
-  const int64_t pieces = !masked && w.split.parts > 1 ? (items - w.split.whole) * w.split.parts : 0;
-  w.bytes = w.part_off + (size_t)pieces * (size_t)(128 * d + 512) * sizeof(float);
+  const int64_t split_items = !masked && w.split.parts > 1 ? items - w.split.whole : 0;
+  const int64_t pieces = split_items * w.split.parts;
+  // then one 8-byte arrival counter per split item (in-kernel merge)
+  w.ctr_off = w.part_off + (size_t)pieces * (size_t)(128 * d + 512) * sizeof(float);
+  w.bytes = w.ctr_off + (size_t)split_items * sizeof(uint64_t);
   return w;
 }
 

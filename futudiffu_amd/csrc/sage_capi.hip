@@ -4,6 +4,9 @@
 #include <stdarg.h>
 #include <string.h>
 
+#include <atomic>
+#include <chrono>
+#include <cstdlib>
 #include <mutex>
 
 #include "../../include/sage_mi355x.h"
@@ -240,6 +243,23 @@ int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* 
 
 namespace {
 
+// A 56-bit tag never passed to an earlier attention launch of this process (a
+// clock reading at first use, plus a call counter): the split items' arrival
+// counters of other calls never match it (AttnParams::merge_ctr).
+uint64_t next_merge_tag() {
+  static std::atomic<uint64_t> counter{0};
+  static const uint64_t base =
+      (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count() * 0x9E3779B97F4A7C15ull;
+  return (base + counter.fetch_add(1, std::memory_order_relaxed) * 2 + 1) & (((uint64_t)1 << 56) - 1);
+}
+
+// The split items of unmasked launches merge in the attention kernel, unless
+// SAGE_MERGE=kernel asks for the separate merge kernel (tests compare both).
+bool merge_in_kernel() {
+  const char* e = std::getenv("SAGE_MERGE");
+  return e == nullptr || strcmp(e, "kernel") != 0;
+}
+
 // sage_attn_fwd and its variants: validation, workspace layout and launch.
 // s_dump (int8 QK, per-token scales, no mask only) receives the S^T
 // accumulators the kernel's loop consumes.
@@ -327,6 +347,10 @@ int attn_fwd_impl(const void* q_codes, const float* q_scale, const void* k_codes
     p.n_whole = (int)ws.split.whole;
     p.split_parts = ws.split.parts;
     p.part = reinterpret_cast<float*>(wsp + ws.part_off);
+    if (ws.split.parts > 1 && merge_in_kernel()) {
+      p.merge_ctr = reinterpret_cast<uint64_t*>(wsp + ws.ctr_off);
+      p.merge_tag = next_merge_tag();
+    }
   }
   if ((int64_t)p.bh * nq + (int64_t)sage::kHeavyMax * h + 8 * sage::kResidentWGs > kMaxGridUnits)
     return fail(SAGE_ERR_ARG, "b*h*ceil(n/128) = %lld exceeds the grid limit", (long long)(p.bh * nq));

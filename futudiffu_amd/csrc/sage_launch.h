@@ -46,6 +46,12 @@ struct AttnParams {
   int n_whole;
   int split_parts;
   float* part;  // (items - n_whole) * split_parts slots of kPartFloats<D> floats
+  // in-kernel merge: one arrival counter per split item (the last piece to
+  // arrive merges the item); null: merge_split_kernel merges after the launch.
+  // A counter holds merge_tag << 8 | pieces arrived; the merging piece resets
+  // it to merge_tag << 8, so a graph replay with the same tag counts from 0.
+  uint64_t* merge_ctr;
+  uint64_t merge_tag;
   // parity only (int8 QK, unmasked): int32 [BH, Np, Np] receives the S^T
   // accumulators of every tile the kernel's own loop consumes (row = query)
   int32_t* s_dump;
@@ -156,7 +162,7 @@ hipError_t launch_doc_summaries(const int32_t* doc, int64_t n, int nb, int4* kv_
 // Workspace of one attention call: the doc-id summaries, then the partial
 // slots of the tail split.
 struct AttnWorkspace {
-  size_t doc_off, heavy_off, part_off, bytes;
+  size_t doc_off, heavy_off, part_off, ctr_off, bytes;
   TailSplit split;
 };
 // `masked`: a launch with a tile mask or document ids, which splits no item

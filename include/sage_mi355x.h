@@ -172,8 +172,11 @@ int sage_quantize_from_qkv(const void* qkv, const float* q_norm_w, const float* 
  * key-tile range of every 128-row query block (written and used when doc_ids
  * is given), then the fp32 partial results of the key-tile pieces of
  * the 128-row items that an unmasked launch splits (the items past the last
- * whole round of 512 resident workgroups).  Enough for every launch of that
- * shape.  No reference counterpart (the Triton launch needs no workspace). */
+ * whole round of 512 resident workgroups) and an 8-byte arrival counter per
+ * split item (the last piece to finish merges the item's partials; the
+ * counters need no clearing, each call tags them with a value no earlier
+ * call used).  Enough for every launch of that shape.  No reference
+ * counterpart (the Triton launch needs no workspace). */
 size_t sage_attn_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
 
 /* Bytes of device workspace a sage_attn_fwd launch with a tile_mask or

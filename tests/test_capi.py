@@ -67,16 +67,17 @@ def test_sizes_and_padding():
     # and the scheduled key-tile range of each 128-row query block (int4 each),
     # the list of split query tiles (a count and 2 entries, int4 each),
     # then (256-byte aligned) fp32 slots of 128 x D + 512 floats for the pieces
-    # of the split tail: 26 items x 4 pieces (the cap) at the 1x30x4416x128
-    # headline shape (1050 items = 2 rounds of 512 + 26); below one round,
-    # the items past one per CU (256) in two halves when at most 128 of them:
-    # 300 items at 1x30x1280 -> 44 x 2, 400 items (1x40x1280) uncut
-    for b, h, n, d, pieces in ((2, 3, 200, 128, 0), (1, 30, 4416, 128, 26 * 4), (1, 1, 1, 64, 0),
-                               (1, 30, 1280, 128, 44 * 2), (1, 40, 1280, 128, 0), (1, 26, 1280, 128, 4 * 2),
-                               (2, 30, 4416, 128, 52 * 4)):
+    # of the split tail, and an 8-byte arrival counter per split item: 26
+    # items x 4 pieces (the cap) at the 1x30x4416x128 headline shape (1050
+    # items = 2 rounds of 512 + 26); below one round, the items past one per
+    # CU (256) in two halves when at most 128 of them: 300 items at 1x30x1280
+    # -> 44 x 2, 400 items (1x40x1280) uncut
+    for b, h, n, d, items, parts in ((2, 3, 200, 128, 0, 1), (1, 30, 4416, 128, 26, 4), (1, 1, 1, 64, 0, 1),
+                                     (1, 30, 1280, 128, 44, 2), (1, 40, 1280, 128, 0, 1), (1, 26, 1280, 128, 4, 2),
+                                     (2, 30, 4416, 128, 52, 4)):
         np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
         doc = ((b * (nt + np_ // 32 + 2 * (np_ // 128)) + 1 + 2) * 16 + 255) // 256 * 256
-        assert lib.sage_attn_workspace_bytes(b, h, n, d) == doc + pieces * (128 * d + 512) * 4
+        assert lib.sage_attn_workspace_bytes(b, h, n, d) == doc + items * parts * (128 * d + 512) * 4 + items * 8
         # a masked launch splits no item: the summaries only
         assert lib.sage_attn_masked_workspace_bytes(b, h, n, d) == doc
 

@@ -412,10 +412,36 @@ def test_headline_schedule_consistency(cuda, qk, pv):
 def test_split_tail_matches_oracle(cuda, qk, pv, D):
     """520 query-tile items (2 x 130 heads x 2 tiles) fill one round of 512
     workgroups and leave 8 items that are cut into 4 key-tile pieces each and
-    merged by the second kernel."""
+    merged by the last piece of each to finish."""
     SA = _sa()
     B, H, N = 2, 130, 256
     q, k, v = O.make_inputs(B, H, N, D, seed=43 + D)
     out, lse = SA.sage_forward(q.to(cuda), k.to(cuda), v.to(cuda), qk=qk, pv=pv)
     torch.cuda.synchronize()
     _compare(out, lse, q, k, v, qk, pv, "token")
+
+
+@pytest.mark.parametrize("B,H,N,qk,pv", [(1, 30, 4416, "int8", "fp8"), (1, 30, 4416, "fp8", "bf16"),
+                                         (1, 30, 1280, "int8", "fp8"), (2, 30, 4416, "int8", "bf16"),
+                                         (2, 130, 256, "fp8", "fp8")])
+def test_split_items_merged_in_kernel_as_by_merge_kernel(cuda, monkeypatch, B, H, N, qk, pv):
+    """The pieces of the split items merged inside the attention kernel (by
+    the last piece of each item to arrive) give the bits of the separate merge
+    kernel (SAGE_MERGE=kernel): the 26 x 4 pieces of the headline, the 44
+    halves of a launch below one round, 52 x 4 pieces over two batches, 8 x 4
+    short pieces.  Three calls in a row, so the arrival counters hold the
+    previous call's tag."""
+    SA = _sa()
+    q, k, v = (t.to(cuda) for t in O.make_inputs(B, H, N, 128, seed=61 + N))
+    qz = SA.quantize_qkv(q, k, v, qk=qk, pv=pv)
+    print(f"split items {B}x{H}x{N} {qk}/{pv}: merge kernel", flush=True)
+    monkeypatch.setenv("SAGE_MERGE", "kernel")
+    want, want_lse = SA.attn_from_quantized(qz, B, H)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("SAGE_MERGE")
+    for i in range(3):
+        print(f"  in-kernel merge, call {i}", flush=True)
+        out, lse = SA.attn_from_quantized(qz, B, H)
+        torch.cuda.synchronize()
+        _assert_bits_equal(out, want, f"out, call {i}")
+        _assert_bits_equal(lse, want_lse, f"lse, call {i}")
