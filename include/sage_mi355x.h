@@ -239,7 +239,9 @@ int sage_attn_fwd(const void* q_codes, const float* q_scale,
  * 1x30x4416x128 headline needs 6.9 MB, the masked packed 1x30x6912 batch
  * 7 KB).  The call allocates and frees
  * nothing and needs no memory cleared beforehand: every byte of scratch it
- * reads was written earlier in the same call.  Every call on one GPU shares
+ * reads was written earlier in the same call, except the split items'
+ * arrival counters, whose per-call tag makes another call's value count as
+ * zero.  Every call on one GPU shares
  * that GPU's scratch, so calls that overlap on one GPU (other streams, other
  * threads) race; calls ordered on one stream do not.  The stream must belong
  * to the current device.  The first call on a device looks the array's
