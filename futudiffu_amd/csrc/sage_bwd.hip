@@ -27,8 +27,9 @@
 // Workgroups have 8 waves, two per SIMD; stages pass through a two-stage LDS
 // ring filled by direct global -> LDS loads issued one stage ahead (one
 // barrier per stage).  Work items are dealt to XCDs in contiguous ranges.
+// One launch (bwd_kernel) runs the dK/dV items, then the dQ items.
 //
-// dQ kernel: a workgroup is the forward's 128-query tile; wave w takes queries
+// dQ pass: a workgroup is the forward's 128-query tile; wave w takes queries
 // 32 (w % 4) and key half w / 4 of every 64-key tile.  Per wave and tile, in
 // the S^T layout (lane (h, r) = query r, keys 8J + 4h + i):
 //   S^T = K . Q^T (int8 / fp8 MFMA, the forward's operands),
@@ -36,7 +37,7 @@
 //   dS^T = P^T (dP^T - D), dQ += dS . K~ (A = dS from the registers, B = T image of K~);
 // the two key halves' dQ are added, then dQ * sm_scale is rounded to bf16
 // (sage_kernels.py:1720).
-// dK/dV kernel: a workgroup owns 128 keys; wave w takes keys 32 (w % 4) and
+// dK/dV pass: a workgroup owns 128 keys; wave w takes keys 32 (w % 4) and
 // query half w / 4 of every 64-query step.  Per wave and step, in the S
 // layout (lane (h, r) = key r, queries 8J + 4h + i):
 //   S = Q . K^T and dP = dO . V^T (the wave's K codes in registers, the
@@ -243,22 +244,21 @@ __device__ __forceinline__ void dma_chunks(uint8_t* lds, int wave, int lane, Src
   sage::dma_chunks<C, kBwdThreads / 64>(lds, wave, lane, src);
 }
 
-// dQ.  Wave w covers queries 32 * (w % 4) of the workgroup's 128-query tile
-// and key half w / 4 of every 64-key tile; the two key halves' partial dQ are
-// summed (half 0 + half 1) at the end.
+// dQ of item (bh, 128-query tile), in `smem` (2 * DqStage<D>::bytes).  Wave
+// w covers queries 32 * (w % 4) of the tile and key half w / 4 of every
+// 64-key tile; the two key halves' partial dQ are summed (half 0 + half 1) at
+// the end.
 template <int D, int QK, int MASK>
-__global__ void __launch_bounds__(kBwdThreads) bwd_dq_kernel(BwdParams p) {
+__device__ __forceinline__ void dq_item(const BwdParams& p, uint8_t* smem, int item) {
   using St = DqStage<D>;
   using SAcc = typename BAcc<QK>::type;
   constexpr int NC = D / 32, CPR = D / 8;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * St::bytes];
   static_assert(4 * NC * 16 * 64 * 4 <= 2 * St::bytes, "partial dQ exchange must fit in the ring");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int h = lane >> 5, r = lane & 31;
   const int qg = wave & 3, b = wave >> 2;  // query group, key half
   const int nq = (int)(p.np / kRowsPerWG);
-  const int item = xcd_item(blockIdx.x, (int)gridDim.x);
   const int bh = item / nq, qt = item % nq;
   const int bidx = bh / p.h;
   const int64_t n = p.n, np = p.np;
@@ -489,25 +489,27 @@ struct DkvStage {
   static constexpr int cQc = qcBytes / 16, cRow = rowBytes / 16;
 };
 
-// dK, dV.  Wave w owns keys 32 * (w % 4) of the workgroup's 128 keys and
-// query half w / 4 of every 64-query step; the two query halves' partial dK
-// and dV are summed (half 0 + half 1) at the end.
+// LDS of a dK/dV item: two step stages, then the R image of the workgroup's
+// 128 V rows, read as the B operand of dP by the waves that own them.
+template <int D>
+constexpr int kDkvLds = 2 * DkvStage<D>::bytes + kRowsPerWG * 2 * D;
+
+// dK, dV of item (bh, 128-key block), in `smem` (kDkvLds<D>).  Wave w owns
+// keys 32 * (w % 4) of the workgroup's 128 keys and query half w / 4 of every
+// 64-query step; the two query halves' partial dK and dV are summed (half 0 +
+// half 1) at the end.
 template <int D, int QK, int MASK>
-__global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
+__device__ __forceinline__ void dkdv_item(const BwdParams& p, uint8_t* smem, int item) {
   using St = DkvStage<D>;
   using SAcc = typename BAcc<QK>::type;
   constexpr int NC = D / 32, CPR = D / 8;
-  // two step stages, then the R image of the workgroup's 128 V rows, read as
-  // the B operand of dP by the waves that own them
   constexpr int kVOff = 2 * St::bytes;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kVOff + kRowsPerWG * 2 * D];
   static_assert(4 * NC * 16 * 64 * 4 <= 2 * St::bytes, "partial dK/dV exchange must fit in the ring");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int h = lane >> 5, r = lane & 31;
   const int kg = wave & 3, a = wave >> 2;  // key group, query half
   const int nkb = (int)(p.np / kRowsPerWG);
-  const int item = xcd_item(blockIdx.x, (int)gridDim.x);
   const int bh = item / nkb, kb = item % nkb;
   const int bidx = bh / p.h;
   const int64_t n = p.n, np = p.np;
@@ -756,6 +758,27 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dkdv_kernel(BwdParams p) {
   }
 }
 
+// The two gradient passes in one launch: workgroups [0, kv_wgs) take the
+// dK/dV items (kv_wgs = items rounded up to a multiple of 8, the extra ones
+// exit), the next `items` the dQ items.  The passes are independent, so the
+// dQ items fill the CUs the last dK/dV round leaves idle, and the shorter
+// items come last.  Each part deals its items to the XCDs like a launch of
+// its own (xcd_item): kv_wgs is a multiple of the XCD count, so a dQ
+// workgroup's XCD is its index within the part modulo 8.
+template <int D>
+constexpr int kBwdLds = kDkvLds<D> > 2 * DqStage<D>::bytes ? kDkvLds<D> : 2 * DqStage<D>::bytes;
+
+template <int D, int QK, int MASK>
+__global__ void __launch_bounds__(kBwdThreads) bwd_kernel(BwdParams p, int items, int kv_wgs) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kBwdLds<D>];
+  const int wg = (int)blockIdx.x;
+  if (wg < kv_wgs) {
+    if (wg < items) dkdv_item<D, QK, MASK>(p, smem, xcd_item(wg, items));
+  } else {
+    dq_item<D, QK, MASK>(p, smem, xcd_item(wg - kv_wgs, items));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
@@ -780,9 +803,10 @@ hipError_t launch_bwd_prep(const TImageJobs& tjobs, const TImageJobs& rjobs, con
 
 template <int D, int QK, int MASK>
 hipError_t launch_bwd_t(const BwdParams& p, int64_t bh, hipStream_t st) {
-  const dim3 grid((unsigned)(p.np / kRowsPerWG * bh));  // items in xcd_item order
-  hipLaunchKernelGGL((bwd_dkdv_kernel<D, QK, MASK>), grid, dim3(kBwdThreads), 0, st, p);
-  hipLaunchKernelGGL((bwd_dq_kernel<D, QK, MASK>), grid, dim3(kBwdThreads), 0, st, p);
+  const int64_t items = p.np / kRowsPerWG * bh;  // per pass, in xcd_item order
+  const int64_t kv_wgs = (items + 7) / 8 * 8;
+  hipLaunchKernelGGL((bwd_kernel<D, QK, MASK>), dim3((unsigned)(kv_wgs + items)), dim3(kBwdThreads), 0, st, p,
+                     (int)items, (int)kv_wgs);
   return hipGetLastError();
 }
 
