@@ -836,7 +836,7 @@ def main():
         "prewarm": {**warm, "note": "untimed run of the same op before the counted warm-up (clock ramp)"},
         "roofline": {
             "bound": "mfma",
-            "kernel": "attn_fwd_kernel + merge_split_kernel",
+            "kernel": "attn_fwd_kernel (split tail items merged inside it)",
             "achieved": round(attn_tflops, 3),
             "peak": peak,
             "unit": "TFLOP/s",

@@ -6,8 +6,8 @@ out-projection.  The kernel can store rows in that layout directly
 (out_layout "bnhd").  The arithmetic is the same, so the values must be
 bit-identical to the transposed [B, H, N, D] output, LSE included, on every
 kernel path: tile-masked, doc-id masked, unmasked whole items, and unmasked
-split-tail items written by the merge kernel.  Rows past N must not be stored:
-a guard region after the output keeps its fill value.
+split-tail items written by the merge of their pieces.  Rows past N must not
+be stored: a guard region after the output keeps its fill value.
 """
 
 import math
