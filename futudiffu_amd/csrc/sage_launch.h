@@ -81,12 +81,15 @@ constexpr int64_t kPartFloats = 128 * D + 2 * 256;
 // Launches of less than one round: an item alone on a CU runs about 1.4x
 // faster than one of two sharing it (its waves have the SIMDs' issue slots to
 // themselves), so when up to 128 items spill past one per CU, the first 256
-// stay whole and the spilled items are cut in two key halves that share the
-// CUs with them (measured at 20 tiles, kernel + merge: 260 items 43.5 ->
-// 34.8 us, 300 items 41.6 -> 36.9, 350 items 41.5 -> 39.1; 400 items lose,
-// 42.1 -> 55.7).  Cutting every item costs more than it balances (300 items:
-// 54.3 / 57.7 / 59.6 us in 2 / 3 / 4 pieces), as do more pieces of the
-// spilled items (300 items: 37.5 / 37.9 us in 3 / 4).
+// stay whole and the spilled items are cut into key-tile pieces that share
+// the CUs with them: 4 pieces (at least 2 tiles each) while every piece still
+// fits the one round of resident workgroups, else as many as fit, at least 2.
+// Measured at 20 tiles with a separate merge kernel: 2 pieces, 260 items
+// 43.5 -> 34.8 us, 300 items 41.6 -> 36.9, 350 items 41.5 -> 39.1; 400 items
+// lose, 42.1 -> 55.7; cutting every item costs more than it balances (300
+// items: 54.3 / 57.7 / 59.6 us in 2 / 3 / 4 pieces).  With the merge inside
+// the attention kernel, 300 items: 34.4 us in 2 pieces, 31.7 / 31.6 in 3 / 4,
+// 33.1 in 5.
 struct TailSplit {
   int64_t whole;
   int parts;
@@ -96,7 +99,13 @@ inline TailSplit tail_split(int64_t n_items, int64_t nt) {
   TailSplit t{n_items, 1};
   constexpr int64_t kCUs = kResidentWGs / 2;
   if (n_items > kCUs && n_items < kResidentWGs) {
-    if (n_items - kCUs <= 128 && nt >= 2) t = TailSplit{kCUs, 2};
+    const int64_t spill = n_items - kCUs;
+    if (spill <= 128 && nt >= 2) {
+      int64_t parts = kCUs / spill;  // pieces that fit the round
+      parts = parts < 4 ? parts : 4;
+      parts = parts < nt / 2 ? parts : nt / 2;
+      t = TailSplit{kCUs, (int)(parts > 2 ? parts : 2)};
+    }
     return t;
   }
   const int64_t rest = n_items >= kResidentWGs ? n_items % kResidentWGs : 0;

@@ -70,10 +70,13 @@ def test_sizes_and_padding():
     # of the split tail, and an 8-byte arrival counter per split item: 26
     # items x 4 pieces (the cap) at the 1x30x4416x128 headline shape (1050
     # items = 2 rounds of 512 + 26); below one round, the items past one per
-    # CU (256) in two halves when at most 128 of them: 300 items at 1x30x1280
-    # -> 44 x 2, 400 items (1x40x1280) uncut
+    # CU (256), when at most 128 of them, in min(4, 256 // spilled, nt // 2)
+    # pieces, at least 2: 300 items at 1x30x1280 -> 44 x 4, 350 (1x35x1280)
+    # -> 94 x 2, 260 items at 1x26x1280 -> 4 x 4, 260 items of 3 tiles
+    # (1x130x160) -> 4 x 2, 400 items (1x40x1280) uncut
     for b, h, n, d, items, parts in ((2, 3, 200, 128, 0, 1), (1, 30, 4416, 128, 26, 4), (1, 1, 1, 64, 0, 1),
-                                     (1, 30, 1280, 128, 44, 2), (1, 40, 1280, 128, 0, 1), (1, 26, 1280, 128, 4, 2),
+                                     (1, 30, 1280, 128, 44, 4), (1, 40, 1280, 128, 0, 1), (1, 26, 1280, 128, 4, 4),
+                                     (1, 35, 1280, 128, 94, 2), (1, 130, 160, 64, 4, 2),
                                      (2, 30, 4416, 128, 52, 4)):
         np_, nt = (n + 127) // 128 * 128, (n + 63) // 64
         doc = ((b * (nt + np_ // 32 + 2 * (np_ // 128)) + 1 + 2) * 16 + 255) // 256 * 256

@@ -94,8 +94,8 @@ def test_headline_full_launch_matches_oracle(cuda, qk, pv):
 
 def test_dit512_full_grid_matches_oracle(cuda):
     """512x512: 1x30x1280x128 int8/fp8, 300 items in less than one round:
-    256 whole items, the other 44 in two key halves merged by the second
-    kernel.  Every head against the oracle."""
+    256 whole items, the other 44 in four key-tile pieces merged by the last
+    of each to finish.  Every head against the oracle."""
     SA = _sa()
     B, H, N, D = 1, 30, 1280, 128
     q, k, v = _inputs(B, H, N, D, seed=21)
