@@ -1194,19 +1194,6 @@ __device__ __forceinline__ void store_partial_coherent(float* slot, const f32x16
   __hip_atomic_store(tail + 256 + tid, __float_as_uint(l_acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Counts a piece's arrival at its split item (AttnParams::merge_ctr); true
-// for the last of `parts` pieces.  A counter whose tag is not this launch's
-// (another call's, or memory never written) starts again from 0.
-__device__ __forceinline__ bool arrive_last(uint64_t* ctr, uint64_t tag, int parts) {
-  const uint64_t mine = tag << 8;
-  uint64_t old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  uint64_t next;
-  do {
-    next = ((old & ~(uint64_t)0xff) == mine ? old : mine) + 1;
-  } while (!__hip_atomic_compare_exchange_weak(ctr, &old, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT));
-  return (int)(next & 0xff) == parts;
-}
 
 // The merge of split item si by the workgroup of its last piece, with the
 // operations of merge_split_kernel in the same order (so the same bits).  The

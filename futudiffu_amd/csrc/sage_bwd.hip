@@ -248,8 +248,13 @@ __device__ __forceinline__ void dma_chunks(uint8_t* lds, int wave, int lane, Src
 // w covers queries 32 * (w % 4) of the tile and key half w / 4 of every
 // 64-key tile; the two key halves' partial dQ are summed (half 0 + half 1) at
 // the end.
+// Key tiles [t_begin, t_end) of the item; with cut >= 0 the item is cut item
+// `cut` (AttnParams-style in-kernel merge): the half's fp32 dQ goes to its
+// slot, and the last half to arrive sums both slots (first half + second
+// half) and stores dQ.
 template <int D, int QK, int MASK>
-__device__ __forceinline__ void dq_item(const BwdParams& p, uint8_t* smem, int item) {
+__device__ __forceinline__ void dq_item(const BwdParams& p, uint8_t* smem, int item, int t_begin, int t_end,
+                                        int cut, int half) {
   using St = DqStage<D>;
   using SAcc = typename BAcc<QK>::type;
   constexpr int NC = D / 32, CPR = D / 8;
@@ -305,7 +310,7 @@ __device__ __forceinline__ void dq_item(const BwdParams& p, uint8_t* smem, int i
     return on;
   };
   auto next_active = [&](int t) __attribute__((always_inline)) -> int {
-    while (t < nt && !active(t)) ++t;
+    while (t < t_end && !active(t)) ++t;
     return t;
   };
 
@@ -345,17 +350,17 @@ __device__ __forceinline__ void dq_item(const BwdParams& p, uint8_t* smem, int i
       reinterpret_cast<u32x4*>(sb + St::offDoc)[tid - 16] = psm;
   };
 
-  int t = next_active(0);
-  if (t < nt) {
+  int t = next_active(t_begin);
+  if (t < t_end) {
     load_tile(t, 0);
     store_small(0);
   }
   wait_vmem();
   __syncthreads();
   int stage = 0;
-  while (t < nt) {
+  while (t < t_end) {
     const int tn = next_active(t + 1);
-    if (tn < nt) load_tile(tn, stage ^ 1);
+    if (tn < t_end) load_tile(tn, stage ^ 1);
     bool wave_on = wave_live;
     if constexpr (MASK & 2)
       wave_on = wave_on && classify(qsum32, load_uniform(p.kv_sum, (int64_t)bidx * nt + t)) != 0;
@@ -421,7 +426,7 @@ __device__ __forceinline__ void dq_item(const BwdParams& p, uint8_t* smem, int i
         for (int tt = 0; tt < 2; ++tt)
           acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(dsa[tt], tkf[c][tt], acc[c], 0, 0, 0);
     }
-    if (tn < nt) store_small(stage ^ 1);
+    if (tn < t_end) store_small(stage ^ 1);
     wait_vmem();
     __syncthreads();
     stage ^= 1;
@@ -445,6 +450,41 @@ __device__ __forceinline__ void dq_item(const BwdParams& p, uint8_t* smem, int i
       for (int e = 0; e < 16; ++e) acc[c][e] += xch[(c * 16 + e) * 64 + lane];
   }
   __syncthreads();
+  if (cut >= 0) {
+    // a half of a cut item: its dQ through to the coherence point, complete
+    // before it counts; the last half sums the two slots in key order
+    constexpr int kSlot = 4 * NC * 16 * 64;
+    uint32_t* slots = reinterpret_cast<uint32_t*>(p.dq_part + (int64_t)cut * 2 * kSlot);
+    if (b == 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          __hip_atomic_store(slots + half * kSlot + ((qg * NC + c) * 16 + e) * 64 + lane, __float_as_uint(acc[c][e]),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    wait_vmem();
+    __syncthreads();
+    int* last = reinterpret_cast<int*>(smem);
+    if (tid == 0) *last = arrive_last(p.dq_ctr + cut, p.dq_tag, 2) ? 1 : 0;
+    __syncthreads();
+    if (*last == 0) return;
+    if (b == 0) {
+      auto ld = [](const uint32_t* a) __attribute__((always_inline)) {
+        return __uint_as_float(__hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      };
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int at = ((qg * NC + c) * 16 + e) * 64 + lane;
+          acc[c][e] = ld(slots + at) + ld(slots + kSlot + at);
+        }
+    }
+    if (tid == 0)
+      __hip_atomic_store(p.dq_ctr + cut, p.dq_tag << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();  // every wave has read `last` before the staging below reuses the LDS
+  }
   uint16_t* stg = reinterpret_cast<uint16_t*>(smem) + qg * 32 * D;
   if (b == 0) {
 #pragma unroll
@@ -760,7 +800,9 @@ __device__ __forceinline__ void dkdv_item(const BwdParams& p, uint8_t* smem, int
 
 // The two gradient passes in one launch: workgroups [0, kv_wgs) take the
 // dK/dV items (kv_wgs = items rounded up to a multiple of 8, the extra ones
-// exit), the next `items` the dQ items.  The passes are independent, so the
+// exit), the next `items` the dQ items, of which the last p.dq_split take the
+// first key-tile half of their item, and the dq_split after those the second
+// halves (dispatched last, the short pieces fill the launch's end).  The passes are independent, so the
 // dQ items fill the CUs the last dK/dV round leaves idle, and the shorter
 // items come last.  Each part deals its items to the XCDs like a launch of
 // its own (xcd_item): kv_wgs is a multiple of the XCD count, so a dQ
@@ -772,11 +814,18 @@ template <int D, int QK, int MASK>
 __global__ void __launch_bounds__(kBwdThreads) bwd_kernel(BwdParams p, int items, int kv_wgs) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kBwdLds<D>];
   const int wg = (int)blockIdx.x;
+  const int nt = (int)((p.n + 63) / 64), mid = nt / 2;
   if (wg < kv_wgs) {
     if (wg < items) dkdv_item<D, QK, MASK>(p, smem, xcd_item(wg, items));
-  } else {
-    dq_item<D, QK, MASK>(p, smem, xcd_item(wg - kv_wgs, items));
+    return;
   }
+  const int j = wg - kv_wgs, whole = items - p.dq_split;
+  if (j < whole)
+    dq_item<D, QK, MASK>(p, smem, xcd_item(j, items), 0, nt, -1, 0);
+  else if (j < items)
+    dq_item<D, QK, MASK>(p, smem, xcd_item(j, items), 0, mid, j - whole, 0);
+  else
+    dq_item<D, QK, MASK>(p, smem, xcd_item(j - p.dq_split, items), mid, nt, j - items, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -805,8 +854,8 @@ template <int D, int QK, int MASK>
 hipError_t launch_bwd_t(const BwdParams& p, int64_t bh, hipStream_t st) {
   const int64_t items = p.np / kRowsPerWG * bh;  // per pass, in xcd_item order
   const int64_t kv_wgs = (items + 7) / 8 * 8;
-  hipLaunchKernelGGL((bwd_kernel<D, QK, MASK>), dim3((unsigned)(kv_wgs + items)), dim3(kBwdThreads), 0, st, p,
-                     (int)items, (int)kv_wgs);
+  hipLaunchKernelGGL((bwd_kernel<D, QK, MASK>), dim3((unsigned)(kv_wgs + items + p.dq_split)), dim3(kBwdThreads), 0,
+                     st, p, (int)items, (int)kv_wgs);
   return hipGetLastError();
 }
 

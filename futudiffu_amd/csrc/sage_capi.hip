@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cstdlib>
@@ -131,7 +132,7 @@ int check_producer(const void* qkv, const float* q_norm_w, const float* k_norm_w
 // Backward workspace: byte offsets of the quantization's outputs (codes,
 // scales, K mean, column-sum partials), the T images of dO, Q and K~, and D.
 struct BwdWorkspace {
-  size_t qc, qs, kc, ks, kmean, quant, tdo, tq, tk, rdo, rv, delta, sums, bytes;
+  size_t qc, qs, kc, ks, kmean, quant, tdo, tq, tk, rdo, rv, delta, sums, dq_part, dq_ctr, bytes;
 };
 
 BwdWorkspace bwd_workspace(int64_t b, int64_t bh, int64_t n, int64_t d) {
@@ -157,6 +158,9 @@ BwdWorkspace bwd_workspace(int64_t b, int64_t bh, int64_t n, int64_t d) {
   w.delta = take(rows * 4);
   // document-id summaries (used with doc_ids): key tiles, 32- and 128-row blocks
   w.sums = take((size_t)b * ((n + 63) / 64 + np / 32 + np / 128) * sizeof(int4));
+  // fp32 partial dQ of the cut items' two key-tile halves, their counters
+  w.dq_part = take((size_t)sage::kBwdDqSplit * 2 * 128 * d * sizeof(float));
+  w.dq_ctr = take((size_t)sage::kBwdDqSplit * sizeof(uint64_t));
   w.bytes = off;
   return w;
 }
@@ -258,6 +262,13 @@ uint64_t next_merge_tag() {
 bool merge_in_kernel() {
   const char* e = std::getenv("SAGE_MERGE");
   return e == nullptr || strcmp(e, "kernel") != 0;
+}
+
+// The backward cuts its last dQ items in two key halves unless
+// SAGE_BWD_SPLIT=off (tests compare both).
+bool bwd_split_enabled() {
+  const char* e = std::getenv("SAGE_BWD_SPLIT");
+  return e == nullptr || strcmp(e, "off") != 0;
 }
 
 // sage_attn_fwd and its variants: validation, workspace layout and launch.
@@ -547,6 +558,14 @@ int sage_attn_bwd(const void* q, const void* k, const void* v, const void* out, 
   p.np = np;
   p.h = (int)h;
   p.sm_scale = sm_scale;
+  // the last dQ items (up to kBwdDqSplit, a multiple of 8) in two key halves
+  // (measured at 1x30x4416x128: 1150.6 -> 1124.5 us with 128; 64 and 256
+  // within the run-to-run spread of 128)
+  const int64_t items = bh * (np / 128);
+  p.dq_split = nkv >= 2 && bwd_split_enabled() ? (int)std::min<int64_t>(sage::kBwdDqSplit, items / 8 * 8) : 0;
+  p.dq_part = reinterpret_cast<float*>(w + ws.dq_part);
+  p.dq_ctr = reinterpret_cast<uint64_t*>(w + ws.dq_ctr);
+  p.dq_tag = next_merge_tag();
   return launch_status(sage::launch_bwd(qk_kind, mask, p, d, bh, stream), "sage_attn_bwd");
 }
 

@@ -139,6 +139,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uin
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 
+// Counts a piece's arrival at its split item's counter (tag << 8 | pieces
+// arrived, relaxed agent-scope atomics); true for the last of `parts` pieces.
+// A counter whose tag is not this launch's (another call's, or memory never
+// written) starts again from 0.
+__device__ __forceinline__ bool arrive_last(uint64_t* ctr, uint64_t tag, int parts) {
+  const uint64_t mine = tag << 8;
+  uint64_t old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t next;
+  do {
+    next = ((old & ~(uint64_t)0xff) == mine ? old : mine) + 1;
+  } while (!__hip_atomic_compare_exchange_weak(ctr, &old, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT));
+  return (int)(next & 0xff) == parts;
+}
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left free; gfx9 encoding).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 

@@ -213,7 +213,19 @@ struct BwdParams {
   int64_t n, np;
   int h;
   float sm_scale;
+  // the last dq_split dQ items of the launch (a multiple of 8) run as two
+  // key-tile halves, dispatched last: fp32 partial dQ slots [dq_split][2]
+  // of 128 * D floats, one arrival counter per cut item (dq_tag << 8 | halves
+  // arrived; the merging half resets it to dq_tag << 8)
+  int dq_split;
+  float* dq_part;
+  uint64_t* dq_ctr;
+  uint64_t dq_tag;
 };
+
+// dQ items of a backward launch cut in two key-tile halves (at most; a
+// multiple of 8, so both halves of an item run on one XCD).
+constexpr int kBwdDqSplit = 64;
 
 // Two operand-image jobs of one launch: x [BH, N, D] bf16 -> out [BH, Np, D]
 // (T or R image), with mu ([BH, D] bf16) subtracted when set (T images only).

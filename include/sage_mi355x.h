@@ -289,8 +289,10 @@ int sage_doc_ids_from_cu_seqlens(const int32_t* cu_seqlens, int64_t b,
 /* Bytes of the workspace sage_attn_bwd needs for b*h heads of n tokens of
  * dimension D: the per-token Q / smoothed-K codes, scales and K mean, the
  * K column-sum partials, bf16 operand images of dO, Q and the smoothed K
- * (the bf16 v_codes layout above), and D = rowsum(dO * O) (fp32 [BH, Np]).
- * No reference counterpart (the Triton launcher allocates these with torch). */
+ * (the bf16 v_codes layout above), D = rowsum(dO * O) (fp32 [BH, Np]), the
+ * document-id summaries, and the fp32 partial dQ of the last dQ items, which
+ * run as two key-tile halves (8 MB at D = 128).  No reference counterpart
+ * (the Triton launcher allocates these with torch). */
 size_t sage_attn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t n, int64_t d);
 
 /* Attention backward: dQ, dK, dV from the forward's inputs, output and LSE.

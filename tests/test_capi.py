@@ -243,7 +243,9 @@ def test_backward_workspace_size():
     """Codes (1 B), scales (4 B) of Q and K; the K mean; the column-sum
     partials; five bf16 operand images (dO, Q and K~ transposed, dO and V by
     row); D (4 B); the document-id summaries (16 B per 64-key tile and per
-    32- and 128-row block of each batch): each region 256-byte aligned."""
+    32- and 128-row block of each batch); the fp32 partial dQ of up to 64
+    items cut in two key halves (64 x 2 x 128 x D floats) and their 8-byte
+    counters: each region 256-byte aligned."""
     from futudiffu_amd import _lib
     lib = _lib.load()
     for b, h, n, d in ((1, 30, 4416, 128), (2, 3, 300, 64), (1, 1, 1, 64)):
@@ -253,6 +255,7 @@ def test_backward_workspace_size():
                 + up(rows * d * 2) * 5 + up(rows * 4))
         np_ = (n + 127) // 128 * 128
         want += up(b * ((n + 63) // 64 + np_ // 32 + np_ // 128) * 16)
+        want += up(64 * 2 * 128 * d * 4) + up(64 * 8)
         assert lib.sage_attn_bwd_workspace_bytes(b, h, n, d) == want
 
 
