@@ -10,8 +10,8 @@
 // forward scores them, s = acc * qd * kd (qd carrying sm_scale*log2(e)),
 // p = 2^(s - lse) with the forward's base-2 LSE.  The quantization kernel
 // supplies the Q and smoothed-K codes and scales and, given dO in place of V,
-// the T image of dO; timage_kernel writes the T images of Q and K~,
-// rimage_kernel the R images of dO and V, delta_kernel D = rowsum(dO * O).
+// the T image of dO; one preparation launch (bwd_prep_kernel) writes the T
+// images of Q and K~, the R images of dO and V and D = rowsum(dO * O).
 //
 // T image of bf16 rows X [N, D]: per 64-token block, chunks (j, b, tt) of 64
 // lanes x 8 bf16, element 4jj + i of lane 32hh + r holding
@@ -105,16 +105,17 @@ __device__ __forceinline__ bool doc_visible(int dq, int dk) { return dk >= 0 && 
 // Preparation
 // ---------------------------------------------------------------------------
 
-// T images of up to two bf16 [BH, N, D] tensors (grid.z selects the job), rows
-// past N zero.  With mu set, the rows are bf16(x - mu) (the quantization's
-// smoothed K, sage_attention.py:63-71).  Grid (np / 64, BH, jobs).
+// T image of 64-token block bx of head bh of job z (of up to two bf16
+// [BH, N, D] tensors), rows past N zero.  With mu set, the rows are
+// bf16(x - mu) (the quantization's smoothed K, sage_attention.py:63-71).
+// img: 2 * 64 * D bytes of LDS.
 template <int D>
-__global__ void __launch_bounds__(256) timage_kernel(TImageJobs jobs, int64_t n, int64_t np) {
+__device__ __forceinline__ void timage_block(const TImageJobs& jobs, int z, int bh, int64_t bx, int64_t n, int64_t np,
+                                             uint8_t* img) {
   constexpr int LPR = D / 8;
   constexpr int VTHREADS = 16 * LPR;  // 16 groups of 4 tokens
-  __shared__ __attribute__((aligned(16))) uint8_t img[2 * 64 * D];
-  const int z = blockIdx.z, bh = blockIdx.y, tid = threadIdx.x;
-  const int64_t tok0 = (int64_t)blockIdx.x * 64;
+  const int tid = threadIdx.x;
+  const int64_t tok0 = bx * 64;
   const uint16_t* x = jobs.x[z] + (int64_t)bh * n * D;
   const uint16_t* mu = jobs.mu[z];
   if (tid < VTHREADS) {
@@ -160,13 +161,13 @@ __global__ void __launch_bounds__(256) timage_kernel(TImageJobs jobs, int64_t n,
 // zero.  It is the row operand of v_mfma_f32_32x32x16_bf16 contracting the
 // channels (lane (h, r) = row r, channels 8h.. of the 16-channel step), so a
 // stage is a contiguous copy and a fragment read is one 16-byte load per lane.
-// Grid (np / 64, BH, jobs), one thread per chunk.
+// One 64-token block (bx) of head bh of job z, one thread per chunk.
 template <int D>
-__global__ void __launch_bounds__(256) rimage_kernel(TImageJobs jobs, int64_t n, int64_t np) {
+__device__ __forceinline__ void rimage_block(const TImageJobs& jobs, int z, int bh, int64_t bx, int64_t n,
+                                             int64_t np) {
   constexpr int G = D / 16;           // 16-channel groups
   constexpr int kChunks = 64 * D / 8;  // 16-byte chunks of a 64-token block
-  const int z = blockIdx.z, bh = blockIdx.y;
-  const int64_t tok0 = (int64_t)blockIdx.x * 64;
+  const int64_t tok0 = bx * 64;
   const uint16_t* x = jobs.x[z] + (int64_t)bh * n * D;
   uint4* o = reinterpret_cast<uint4*>(jobs.out[z] + ((int64_t)bh * np + tok0) * D);
 #pragma unroll
@@ -190,14 +191,14 @@ __device__ __forceinline__ int xcd_item(int b, int total) {
 
 // D = rowsum(dO * O) per token in fp32 (sage_kernels.py:321-349), zero past N.
 // Lane (rr, c8) holds channels [8*c8, +8) of tokens rr + RPP*ps; the products
-// are fp32, summed per lane then over the token's lanes.  Grid (np / 64, BH).
+// are fp32, summed per lane then over the token's lanes.  One 64-token
+// block (bx) of head bh.
 template <int D>
-__global__ void __launch_bounds__(256) delta_kernel(const uint16_t* __restrict__ dout,
-                                                    const uint16_t* __restrict__ out, int64_t n, int64_t np,
-                                                    float* __restrict__ delta) {
+__device__ __forceinline__ void delta_block(const uint16_t* __restrict__ dout, const uint16_t* __restrict__ out,
+                                            int bh, int64_t bx, int64_t n, int64_t np, float* __restrict__ delta) {
   constexpr int LPR = D / 8, RPP = 256 / LPR, PASSES = 64 / RPP;
-  const int bh = blockIdx.y, tid = threadIdx.x, c8 = tid % LPR, rr = tid / LPR;
-  const int64_t tok0 = (int64_t)blockIdx.x * 64;
+  const int tid = threadIdx.x, c8 = tid % LPR, rr = tid / LPR;
+  const int64_t tok0 = bx * 64;
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
     const int64_t t = tok0 + rr + ps * RPP;
@@ -832,21 +833,34 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_kernel(BwdParams p, int items
 // Launchers
 // ---------------------------------------------------------------------------
 
+// The preparation in one launch, grid (np / 64, BH, 5): z = 0, 1 the T images
+// of tjobs, z = 2, 3 the R images of rjobs, z = 4 D.
+template <int D>
+__global__ void __launch_bounds__(256) bwd_prep_kernel(TImageJobs tjobs, TImageJobs rjobs,
+                                                       const uint16_t* __restrict__ dout,
+                                                       const uint16_t* __restrict__ out, int64_t n, int64_t np,
+                                                       float* __restrict__ delta) {
+  __shared__ __attribute__((aligned(16))) uint8_t img[2 * 64 * D];
+  const int z = blockIdx.z, bh = blockIdx.y;
+  const int64_t bx = blockIdx.x;
+  if (z < 2)
+    timage_block<D>(tjobs, z, bh, bx, n, np, img);
+  else if (z < 4)
+    rimage_block<D>(rjobs, z - 2, bh, bx, n, np);
+  else
+    delta_block<D>(dout, out, bh, bx, n, np, delta);
+}
+
 hipError_t launch_bwd_prep(const TImageJobs& tjobs, const TImageJobs& rjobs, const uint16_t* dout,
                            const uint16_t* out, int64_t bh, int64_t n, int64_t d, float* delta, hipStream_t st) {
   const int64_t np = padded_len(n);
-  const dim3 g2((unsigned)(np / 64), (unsigned)bh, 2u), gd((unsigned)(np / 64), (unsigned)bh);
-  if (d == 128) {
-    hipLaunchKernelGGL(timage_kernel<128>, g2, dim3(256), 0, st, tjobs, n, np);
-    hipLaunchKernelGGL(rimage_kernel<128>, g2, dim3(256), 0, st, rjobs, n, np);
-    hipLaunchKernelGGL(delta_kernel<128>, gd, dim3(256), 0, st, dout, out, n, np, delta);
-  } else if (d == 64) {
-    hipLaunchKernelGGL(timage_kernel<64>, g2, dim3(256), 0, st, tjobs, n, np);
-    hipLaunchKernelGGL(rimage_kernel<64>, g2, dim3(256), 0, st, rjobs, n, np);
-    hipLaunchKernelGGL(delta_kernel<64>, gd, dim3(256), 0, st, dout, out, n, np, delta);
-  } else {
+  const dim3 grid((unsigned)(np / 64), (unsigned)bh, 5u);
+  if (d == 128)
+    hipLaunchKernelGGL(bwd_prep_kernel<128>, grid, dim3(256), 0, st, tjobs, rjobs, dout, out, n, np, delta);
+  else if (d == 64)
+    hipLaunchKernelGGL(bwd_prep_kernel<64>, grid, dim3(256), 0, st, tjobs, rjobs, dout, out, n, np, delta);
+  else
     return hipErrorInvalidValue;
-  }
   return hipGetLastError();
 }
 
