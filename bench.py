@@ -41,7 +41,11 @@ METRIC = "Sage attn fwd TFLOPS + ms/call at B=1,H=30,N=4416,D=128; % of fp8 MFMA
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    # 1000 timed steps (about 0.28 s): shorter windows land in the clock and
+    # power swings of the first second of load (measured on one box: 276-279
+    # us per step over 1000-3000 steps, 283-294 over 20 steps after 5
+    # warm-up, 306-312 over 100 steps after 150)
+    ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=150)
     # The GPU clock ramps during the first tens of milliseconds of work
     # (attention 318 us per call after 10 warm-up steps, 287 us after 150), so
@@ -264,14 +268,16 @@ class TimingEvent:
 
 def prewarm(step, seconds):
     """Run ``step`` untimed until ``seconds`` of wall time have passed (the
-    device synchronized), so the counted warm-up starts at steady clocks."""
+    device synchronized), so the counted warm-up starts at steady clocks.
+    The device is synchronized only every 64 steps: an idle gap after every
+    few steps lets the clocks drop again."""
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     n = 0
     while True:
-        for _ in range(4):
+        for _ in range(64):
             step()
-        n += 4
+        n += 64
         torch.cuda.synchronize()
         if time.perf_counter() - t0 >= seconds:
             return {"seconds": round(time.perf_counter() - t0, 4), "steps": n}
