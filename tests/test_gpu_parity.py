@@ -423,14 +423,16 @@ def test_split_tail_matches_oracle(cuda, qk, pv, D):
 
 @pytest.mark.parametrize("B,H,N,qk,pv", [(1, 30, 4416, "int8", "fp8"), (1, 30, 4416, "fp8", "bf16"),
                                          (1, 30, 1280, "int8", "fp8"), (2, 30, 4416, "int8", "bf16"),
-                                         (2, 130, 256, "fp8", "fp8")])
+                                         (2, 130, 256, "fp8", "fp8"), (1, 26, 1280, "int8", "fp8"),
+                                         (1, 35, 1280, "int8", "bf16"), (1, 130, 160, "int8", "fp8")])
 def test_split_items_merged_in_kernel_as_by_merge_kernel(cuda, monkeypatch, B, H, N, qk, pv):
     """The pieces of the split items merged inside the attention kernel (by
     the last piece of each item to arrive) give the bits of the separate merge
-    kernel (SAGE_MERGE=kernel): the 26 x 4 pieces of the headline, the 44
-    halves of a launch below one round, 52 x 4 pieces over two batches, 8 x 4
-    short pieces.  Three calls in a row, so the arrival counters hold the
-    previous call's tag."""
+    kernel (SAGE_MERGE=kernel): the 26 x 4 pieces of the headline, 52 x 4
+    pieces over two batches, 8 x 4 short pieces, and launches below one
+    round: 44 x 4 pieces (1x30x1280), 4 x 4 (1x26x1280), 94 x 2 (1x35x1280),
+    4 x 2 pieces of 3-tile items (1x130x160).  Three calls in a row, so the
+    arrival counters hold the previous call's tag."""
     SA = _sa()
     q, k, v = (t.to(cuda) for t in O.make_inputs(B, H, N, 128, seed=61 + N))
     qz = SA.quantize_qkv(q, k, v, qk=qk, pv=pv)
