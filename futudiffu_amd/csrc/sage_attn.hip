@@ -193,25 +193,30 @@ __device__ __forceinline__ void item_of(int id, int total, int bh_count, int nq,
   }
 }
 
-// The int8 QK^T accumulates on top of the bit pattern of c0 = 1/(2 pi) (the
-// C operand of each chain's first MFMA; the compiler keeps the splat in
-// registers rather than encoding the inline constant).  |acc| <= 128 *
-// 127^2 < 2^21 keeps c0_bits + acc inside c0's binade [1/8, 1/4), whose ulp
-// is 2^-26, so the accumulator read as fp32 is exactly x = c0 + acc * 2^-26,
-// and x - c0 = acc * 2^-26 exactly (Sterbenz).  One subtraction of the
-// inline constant replaces the int -> float conversion (v_cvt_f32_i32 issues
-// at about half the rate of a subtraction); the 2^26 goes into the row's
-// multiplier, so scores, maxima and exp arguments are the same floats as
-// float(acc) * kd * w gives (powers of two scale exactly for row
-// multipliers below 2^101).
+// The start of the int8 QK^T chains.  C0 false: 0, which the MFMA takes as
+// an inline C operand (no registers), and a score is float(acc) * kd, exact
+// in the conversion since |acc| <= 128 * 127^2 < 2^21.  C0 true: the bit
+// pattern of c0 = 1/(2 pi); acc + c0_bits stays inside c0's binade [1/8, 1/4),
+// whose ulp is 2^-26, so the accumulator read as fp32 is exactly
+// x = c0 + acc * 2^-26 and x - c0 = acc * 2^-26 exactly (Sterbenz): one
+// subtraction (issued at about twice the rate of v_cvt_f32_i32) reads the
+// sum, and the 2^26 goes into the row multiplier, so scores, maxima and exp
+// arguments are the same floats either way.  The compiler keeps that splat
+// in 16 registers: the document-id loops gain from the subtraction
+// (1x30x6912 packed 363.7 -> 360.4 us, the 4x30x4352 key-padded batch
+// 980.9 -> 975.5 us), the others from the registers (1x30x4416x128
+// 242.3 -> 241.2 us, the packed tile-mask batch 343.9 -> 334.5 us).
 constexpr int32_t kC0Bits = 0x3E22F983;
 constexpr float kC0 = 0.15915494309189535f;
 static_assert(__builtin_bit_cast(int32_t, kC0) == kC0Bits, "c0 must be the inline constant 1/(2 pi)");
 constexpr float kC0Scale = 67108864.0f;  // 2^26, the accumulator's ulp inverted
-// the C operand of a chain's first int8 MFMA
-__device__ __forceinline__ i32x16 c0_acc() {
-  return i32x16{kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits,
-                kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits};
+template <bool C0>
+__device__ __forceinline__ i32x16 i8_start() {
+  if constexpr (C0)
+    return i32x16{kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits,
+                  kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits, kC0Bits};
+  else
+    return i32x16{0};
 }
 
 template <int QK>
@@ -225,7 +230,7 @@ struct SAccT<kQK_INT8> {
 
 // One 32-key half b of the S^T tile for this wave's 32 queries: acc covers
 // keys 32b + (8j + 4h + i) in lane (h, r), element 4j + i.
-template <int D, int QK>
+template <int D, int QK, bool C0>
 __device__ __forceinline__ void qk_half(const uint8_t* sb, const i32x4* qf, int lane, int b,
                                         typename SAccT<QK>::type& acc) {
   constexpr int NC = D / 32;
@@ -233,7 +238,7 @@ __device__ __forceinline__ void qk_half(const uint8_t* sb, const i32x4* qf, int 
   if constexpr (QK == kQK_INT8) {
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(b * NC + c) * 64 + lane], qf[c], c == 0 ? c0_acc() : acc,
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kl[(b * NC + c) * 64 + lane], qf[c], c == 0 ? i8_start<C0>() : acc,
                                                   0, 0, 0);
   } else {
     acc = f32x16{0};
@@ -248,7 +253,7 @@ __device__ __forceinline__ void qk_half(const uint8_t* sb, const i32x4* qf, int 
 }
 
 // Both 32-key halves of the next S^T as two interleaved MFMA chains.
-template <int D, int QK>
+template <int D, int QK, bool C0>
 __device__ __forceinline__ void qk_both(const uint8_t* sb, const i32x4* qf, int lane, typename SAccT<QK>::type& a0,
                                         typename SAccT<QK>::type& a1) {
   constexpr int NC = D / 32;
@@ -266,13 +271,13 @@ __device__ __forceinline__ void qk_both(const uint8_t* sb, const i32x4* qf, int 
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       __builtin_amdgcn_sched_barrier(0);
-      a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0][c], qf[c], c == 0 ? c0_acc() : a0, 0, 0, 0);
-      a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1][c], qf[c], c == 0 ? c0_acc() : a1, 0, 0, 0);
+      a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0][c], qf[c], c == 0 ? i8_start<C0>() : a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1][c], qf[c], c == 0 ? i8_start<C0>() : a1, 0, 0, 0);
       if (c + 2 < NC) read(c + 2);
     }
   } else {
-    qk_half<D, QK>(sb, qf, lane, 0, a0);
-    qk_half<D, QK>(sb, qf, lane, 1, a1);
+    qk_half<D, QK, C0>(sb, qf, lane, 0, a0);
+    qk_half<D, QK, C0>(sb, qf, lane, 1, a1);
   }
 }
 
@@ -303,7 +308,7 @@ __device__ __forceinline__ void rows_of(float* xrow, float v, int h, int r, floa
 // -inf: only the ragged last tile tests.  With masked set (DOC), the
 // per-token document-id visibility: key visible iff doc[key] >= 0 and
 // (doc[q] == doc[key] or doc[q] < 0).
-template <int D, int QK, int PV, int GRAN, bool DOC>
+template <int D, int QK, int PV, int GRAN, bool DOC, bool C0>
 __device__ __forceinline__ void half_scores(const uint8_t* sb, const typename SAccT<QK>::type& s, int b, int h,
                                             float kd_blk, int kvalid, bool masked, int dq, float (&u)[16]) {
   using St = Stage<D, PV>;
@@ -317,8 +322,10 @@ __device__ __forceinline__ void half_scores(const uint8_t* sb, const typename SA
       kd4 = f32x4{kd_blk, kd_blk, kd_blk, kd_blk};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if constexpr (QK == kQK_INT8)
+      if constexpr (QK == kQK_INT8 && C0)
         u[4 * j + i] = (__int_as_float(s[4 * j + i]) - kC0) * kd4[i];  // acc * kd * 2^-26
+      else if constexpr (QK == kQK_INT8)
+        u[4 * j + i] = (float)s[4 * j + i] * kd4[i];
       else
         u[4 * j + i] = s[4 * j + i] * kd4[i];
     }
@@ -603,10 +610,11 @@ __device__ __forceinline__ void tile_body(const uint8_t* sb, const uint8_t* sb_n
   using St = Stage<D, PV>;
   constexpr int NC = D / 32;
   const int h = lane >> 5, r = lane & 31;
+  constexpr bool C0 = (MASK & 2) != 0;  // the int8 chains' start (i8_start)
   float u[2][16];
-  half_scores<D, QK, PV, GRAN, MASKED>(sb, s0, 0, h, kd_blk, kvalid, true, dq, u[0]);
-  half_scores<D, QK, PV, GRAN, MASKED>(sb, s1, 1, h, kd_blk, kvalid, true, dq, u[1]);
-  qk_both<D, QK>(sb_next, qf, lane, s0, s1);
+  half_scores<D, QK, PV, GRAN, MASKED, C0>(sb, s0, 0, h, kd_blk, kvalid, true, dq, u[0]);
+  half_scores<D, QK, PV, GRAN, MASKED, C0>(sb, s1, 1, h, kd_blk, kvalid, true, dq, u[1]);
+  qk_both<D, QK, C0>(sb_next, qf, lane, s0, s1);
   if constexpr (PV == kPV_FP8) {
     i32x8 pa;
     float rsc;
@@ -680,9 +688,11 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     qd = p.qs[(int64_t)bh * p.np + q0 + r];
   else
     qd = p.qs[(int64_t)bh * (p.np / 64) + (q0 >> 6)];
+  // the int8 chains' start (i8_start): from c0 with document ids
+  constexpr bool kC0Start = (MASK & 2) != 0;
   // log2-domain multiplier of the (K-scaled) accumulators; int8 QK scores
-  // carry 2^-26 (the c0 start), which the multiplier takes back exactly
-  const float w = fmaxf(qd, 1e-30f) * (QK == kQK_INT8 ? kC0Scale : 1.0f);
+  // started from c0 carry 2^-26, which the multiplier takes back exactly
+  const float w = fmaxf(qd, 1e-30f) * (QK == kQK_INT8 && kC0Start ? kC0Scale : 1.0f);
 
   int dq = 0;
   int4 qsum = make_int4(0, 0, 0, 0), qsum128 = make_int4(0, 0, 0, 0);
@@ -779,7 +789,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
     if constexpr (DUMP) {
       int32_t* row = p.s_dump + ((int64_t)bh * p.np + q0 + r) * p.np + (int64_t)tt * 64 + 4 * h;
       auto word = [](auto x) -> int32_t {
-        if constexpr (QK == kQK_INT8) return x - kC0Bits;  // the sum itself
+        if constexpr (QK == kQK_INT8) return kC0Start ? x - kC0Bits : x;  // the sum itself
         else return __float_as_int(x);
       };
 #pragma unroll
@@ -839,7 +849,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
   __syncthreads();
   SAcc s0, s1;  // S^T of the tile about to be consumed
   if (t < t_end && wave_live) {
-    qk_both<D, QK>(smem, qf, lane, s0, s1);
+    qk_both<D, QK, kC0Start>(smem, qf, lane, s0, s1);
   }
 
   // one tile of the general loop: tile t2 into a stage no wave reads any more
@@ -868,7 +878,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
       tile_body<D, QK, PV, GRAN, MASK, false>(sb, sb_next, qf, lane, s0, s1, o, m_ref, l_acc, w, xrow, dq, kdb,
                                               kvalid);
     else if (wave_live && t1 < t_end)
-      qk_both<D, QK>(sb_next, qf, lane, s0, s1);
+      qk_both<D, QK, kC0Start>(sb_next, qf, lane, s0, s1);
 
     // ---- publish tile t2 ---------------------------------------------------------
     if (t2 < t_end) store_doc(smem + stage2 * St::bytes);
@@ -979,9 +989,9 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
       dump(t, s0, s1);
       const float kdb = kd_block(t);
       const int kvalid = keys_valid(t);
-      half_scores<D, QK, PV, GRAN, false>(sp(stage), s0, 0, h, kdb, kvalid, false, dq, u[0]);
-      half_scores<D, QK, PV, GRAN, false>(sp(stage), s1, 1, h, kdb, kvalid, false, dq, u[1]);
-      if (t1 < t_end) qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
+      half_scores<D, QK, PV, GRAN, false, kC0Start>(sp(stage), s0, 0, h, kdb, kvalid, false, dq, u[0]);
+      half_scores<D, QK, PV, GRAN, false, kC0Start>(sp(stage), s1, 1, h, kdb, kvalid, false, dq, u[1]);
+      if (t1 < t_end) qk_both<D, QK, kC0Start>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
       prefetch_pending();
       softmax_p();
       stage_p = stage;
@@ -997,7 +1007,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
       const float kdb = kd_block(t);
       dump(t, s0, s1);
       auto scores = [&](int b_, float (&u_)[16]) __attribute__((always_inline)) {
-        half_scores<D, QK, PV, GRAN, false>(sb, b_ ? s1 : s0, b_, h, kdb, 64, false, dq, u_);
+        half_scores<D, QK, PV, GRAN, false, kC0Start>(sb, b_ ? s1 : s0, b_, h, kdb, 64, false, dq, u_);
       };
       pending_move();
       if constexpr (PV == kPV_FP8) {
@@ -1035,7 +1045,7 @@ __device__ __forceinline__ bool item_tiles(const AttnParams& p, uint8_t* smem, i
         softmax_fp8_exp_qk<D>(u, w, bm, m_ref, l_acc, pa_p, rsc_p, sp(next_stage(stage, 1)), qf, lane, s0, s1);
       } else {
         SAGE_PHASE(1);  // the pending product and this tile's score conversion
-        qk_both<D, QK>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
+        qk_both<D, QK, kC0Start>(sp(next_stage(stage, 1)), qf, lane, s0, s1);
         if constexpr (PV == kPV_BF16) {
           if constexpr (QK != kQK_INT8) pv_bf16_pair<D>(sbp, pb_p, lane, 0, o);
           if constexpr (NP == 2) pv_bf16_pair<D>(sbp, pb_p, lane, 2, o);
