@@ -91,7 +91,7 @@ def test_packing_info_device_mask_drives_attention_like_host_mask(cuda):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16)) and torch.equal(la, lb)
 
 
-@pytest.mark.parametrize("qk,pv", [("int8", "fp8"), ("fp8", "bf16")])
+@pytest.mark.parametrize("qk,pv", [("int8", "fp8"), ("fp8", "bf16"), ("int8", "bf16"), ("fp8", "fp8")])
 def test_packed_exact_ids_equal_serial_images(cuda, qk, pv):
     """Three images of 64-aligned lengths packed into one sequence (plus 64
     padding tokens), masked by exact ids from device cu_seqlens.  Without K
@@ -109,6 +109,40 @@ def test_packed_exact_ids_equal_serial_images(cuda, qk, pv):
     doc = BM.doc_ids_from_cu_seqlens(cu, n)
     print(f"packed vs serial {qk}/{pv} lens={lens}", flush=True)
     out, lse = SA.sage_forward(q, k, v, qk=qk, pv=pv, smooth_k=False, doc_ids=doc)
+    off = 0
+    for s in lens:
+        sl = slice(off, off + s)
+        o1, l1 = SA.sage_forward(q[:, :, sl].contiguous(), k[:, :, sl].contiguous(), v[:, :, sl].contiguous(),
+                                 qk=qk, pv=pv, smooth_k=False)
+        torch.cuda.synchronize()
+        got = out[:, :, sl].contiguous()
+        bad = got.view(torch.int16) != o1.view(torch.int16)
+        assert not bad.any(), (f"segment at {off}: {int(bad.sum())} outputs differ, "
+                               f"max {(got.float() - o1.float()).abs().max().item():.3g}")
+        assert torch.equal(lse.view(B * H, n)[:, sl].cpu(), l1.cpu()), f"segment at {off}: LSE differs"
+        off += s
+
+
+@pytest.mark.parametrize("qk,pv", [("int8", "fp8"), ("int8", "bf16"), ("fp8", "fp8")])
+def test_packed_tile_mask_equal_serial_images(cuda, qk, pv):
+    """Three images of 128-aligned lengths packed into one sequence, masked by
+    the reference tile mask built on the device from their document ids; for
+    aligned images that mask is exactly block diagonal.  Without K smoothing
+    each image's rows see exactly their own key tiles, in the order of the
+    image run alone, so outputs and LSE equal the serial runs bit for bit.
+    The tile-mask loop starts its int8 score chains from zero like the
+    unmasked one; the exact-id test above pins the document-id loop, which
+    starts them from c0, to the same scores."""
+    from futudiffu_amd import block_mask as BM
+    from futudiffu_amd import sage_attention as SA
+    lens = [640, 1152, 1280]
+    n = sum(lens)
+    B, H, D = 1, 2, 128
+    q, k, v = (t.to(cuda) for t in O.make_inputs(B, H, n, D, seed=79))
+    doc = torch.tensor(O.packed_document_ids(lens, n), dtype=torch.int32, device=cuda)
+    mask = BM.build_block_mask_device(doc)
+    print(f"packed tile mask vs serial {qk}/{pv} lens={lens}", flush=True)
+    out, lse = SA.sage_forward(q, k, v, qk=qk, pv=pv, smooth_k=False, block_mask=mask)
     off = 0
     for s in lens:
         sl = slice(off, off + s)
