@@ -352,6 +352,10 @@ MASK_CASES = [
     (2, 2, 700, 128, "int8", "fp8", "doc"),
     (2, 2, 700, 64, "fp8", "bf16", "doc"),
     (1, 2, 1023, 128, "int8", "fp8", "tile+doc"),
+    (2, 2, 700, 128, "int8", "bf16", "doc"),
+    (2, 2, 700, 64, "int8", "fp8", "doc"),
+    (2, 2, 700, 128, "fp8", "fp8", "doc"),
+    (1, 2, 1023, 64, "int8", "bf16", "tile"),
 ]
 
 
