@@ -70,30 +70,31 @@ def test_backward_matches_oracle(cuda, B, H, N, D, qk, smooth):
         _close(g, w, name)
 
 
-@pytest.mark.parametrize("three_d", [False, True])
-def test_tile_masked_backward_matches_oracle(cuda, three_d):
+@pytest.mark.parametrize("three_d,qk", [(False, "int8"), (True, "int8"), (False, "fp8")])
+def test_tile_masked_backward_matches_oracle(cuda, three_d, qk):
     B, H, N, D = 1, 2, 700, 128
     q, k, v, dout = _inputs(B, H, N, D, seed=3)
     bm = O.build_block_mask([300, 250, 150], N)
     if three_d:
         bm = bm.unsqueeze(0).repeat(B * H, 1, 1)
         bm[1, 0, 3] = 1  # a head-specific extra tile pair
-    print(f"bwd tile mask 3d={three_d}", flush=True)
-    out, lse, dq, dk, dv = _run(cuda, q, k, v, dout, "int8", True, block_mask=bm)
-    rq, rk, rv = O.sage_backward(q, k, v, out, lse, dout, 1.0 / math.sqrt(D), block_mask=bm)
+    print(f"bwd tile mask 3d={three_d} qk={qk}", flush=True)
+    out, lse, dq, dk, dv = _run(cuda, q, k, v, dout, qk, True, block_mask=bm)
+    rq, rk, rv = O.sage_backward(q, k, v, out, lse, dout, 1.0 / math.sqrt(D), qk=qk, block_mask=bm)
     for name, g, w in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
         _close(g, w, name)
 
 
-def test_doc_masked_backward_matches_oracle(cuda):
-    B, H, N, D = 2, 2, 520, 64
+@pytest.mark.parametrize("qk,D", [("int8", 64), ("int8", 128), ("fp8", 64)])
+def test_doc_masked_backward_matches_oracle(cuda, qk, D):
+    B, H, N = 2, 2, 520
     q, k, v, dout = _inputs(B, H, N, D, seed=5)
     doc = torch.full((B, N), -1, dtype=torch.int32)
     doc[0, :200], doc[0, 200:450] = 0, 1
     doc[1, 30:300], doc[1, 300:520] = 0, 1
-    print("bwd doc ids", flush=True)
-    out, lse, dq, dk, dv = _run(cuda, q, k, v, dout, "int8", True, doc_ids=doc)
-    rq, rk, rv = O.sage_backward(q, k, v, out, lse, dout, 1.0 / math.sqrt(D), doc_ids=doc)
+    print(f"bwd doc ids qk={qk} D={D}", flush=True)
+    out, lse, dq, dk, dv = _run(cuda, q, k, v, dout, qk, True, doc_ids=doc)
+    rq, rk, rv = O.sage_backward(q, k, v, out, lse, dout, 1.0 / math.sqrt(D), qk=qk, doc_ids=doc)
     for name, g, w in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
         _close(g, w, name)
     # padded keys get no gradient
